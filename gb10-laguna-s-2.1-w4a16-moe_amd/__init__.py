@@ -1,0 +1,23 @@
+"""MI355X (gfx950) W4A16 grouped-expert MoE path.
+
+Drop-in for the reference's ``kernels`` package
+(vladimir-voinea/gb10-laguna-s-2.1-w4a16-moe, kernels/__init__.py:3): the same
+exported names, backed by hand-written HIP kernels behind a C ABI
+(include/w4a16_moe.h).
+"""
+
+from .w4a16_moe import (  # noqa: F401
+    BLOCK_K,
+    BLOCK_M,
+    BLOCK_N,
+    dropped_pairs,
+    fused_experts_w4a16,
+    fused_experts_w4a16_profiled,
+    is_repacked,
+    moe_align_block_size,
+    moe_align_block_size_full,
+    repack_weights,
+    workspace_tensor,
+)
+
+__all__ = ["fused_experts_w4a16", "repack_weights", "moe_align_block_size", "is_repacked"]

@@ -1,0 +1,149 @@
+"""ctypes binding of ``libw4a16moe.so`` (the C ABI in include/w4a16_moe.h).
+
+torch must be imported before the library is loaded: torch ships its own HIP
+runtime under the soname ``libamdhip64.so.7`` and the dynamic linker then binds
+this library to that same runtime, so device pointers and streams from torch
+are valid here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime first, see above)
+
+LIB_PATH = Path(__file__).resolve().parent / "libw4a16moe.so"
+
+W4A16_OK = 0
+W4A16_ERR_NULL_POINTER = 1
+W4A16_ERR_INVALID_SHAPE = 2
+W4A16_ERR_UNSUPPORTED_GROUP = 3
+W4A16_ERR_WORKSPACE_TOO_SMALL = 4
+W4A16_ERR_MISALIGNED = 5
+W4A16_ERR_INVALID_BLOCK = 6
+W4A16_ERR_HIP = 7
+
+WS_SORTED_IDS = 0
+WS_EXPERT_IDS = 1
+WS_HEADER = 2
+WS_OFFSETS = 3
+WS_INTER = 4
+WS_PARTIAL = 5
+WS_NFIELDS = 6
+
+FUSED_BLOCK_M = 16
+
+EXPORTED_SYMBOLS = (
+    "w4a16_moe_align_sizes",
+    "w4a16_moe_align_block_size",
+    "w4a16_moe_workspace_size",
+    "w4a16_moe_workspace_layout",
+    "w4a16_moe_fused_experts",
+    "w4a16_moe_fused_experts_profiled",
+    "w4a16_moe_dropped_pairs",
+    "w4a16_moe_strerror",
+    "w4a16_moe_abi_version",
+)
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.w4a16_moe_abi_version.restype = ctypes.c_int
+    lib.w4a16_moe_abi_version.argtypes = []
+    lib.w4a16_moe_strerror.restype = ctypes.c_char_p
+    lib.w4a16_moe_strerror.argtypes = [ctypes.c_int]
+    lib.w4a16_moe_align_sizes.restype = ctypes.c_int
+    lib.w4a16_moe_align_sizes.argtypes = [
+        _i64, _i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
+    lib.w4a16_moe_align_block_size.restype = ctypes.c_int
+    lib.w4a16_moe_align_block_size.argtypes = [
+        _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.w4a16_moe_workspace_size.restype = ctypes.c_int
+    lib.w4a16_moe_workspace_size.argtypes = [
+        _i64, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)]
+    lib.w4a16_moe_workspace_layout.restype = ctypes.c_int
+    lib.w4a16_moe_workspace_layout.argtypes = [
+        _i64, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)]
+    fused = [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+             _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, ctypes.c_size_t, _vp]
+    lib.w4a16_moe_fused_experts.restype = ctypes.c_int
+    lib.w4a16_moe_fused_experts.argtypes = fused
+    lib.w4a16_moe_fused_experts_profiled.restype = ctypes.c_int
+    lib.w4a16_moe_fused_experts_profiled.argtypes = fused + [ctypes.POINTER(ctypes.c_float)]
+    lib.w4a16_moe_dropped_pairs.restype = ctypes.c_int
+    lib.w4a16_moe_dropped_pairs.argtypes = [_vp, ctypes.POINTER(ctypes.c_int32), _vp]
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library; raises LibraryNotBuilt if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise LibraryNotBuilt(
+                    f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                    "(hipcc --offload-arch=gfx950)"
+                )
+            handle = ctypes.CDLL(str(LIB_PATH))
+            _declare(handle)
+            if handle.w4a16_moe_abi_version() != 1:
+                raise RuntimeError("libw4a16moe.so ABI version mismatch")
+            _lib = handle
+    return _lib
+
+
+def strerror(status: int) -> str:
+    return lib().w4a16_moe_strerror(status).decode()
+
+
+def align_sizes(M: int, topk: int, num_experts: int, block_size: int) -> tuple[int, int]:
+    em, nb = _i64(), _i64()
+    st = lib().w4a16_moe_align_sizes(M, topk, num_experts, block_size,
+                                     ctypes.byref(em), ctypes.byref(nb))
+    check(st)
+    return em.value, nb.value
+
+
+def workspace_size(M: int, topk: int, E: int, N: int, K: int, group: int) -> int:
+    out = ctypes.c_size_t()
+    check(lib().w4a16_moe_workspace_size(M, topk, E, N, K, group, ctypes.byref(out)))
+    return out.value
+
+
+def workspace_layout(M: int, topk: int, E: int, N: int, K: int, group: int) -> list[int]:
+    arr = (ctypes.c_size_t * WS_NFIELDS)()
+    check(lib().w4a16_moe_workspace_layout(M, topk, E, N, K, group, arr))
+    return list(arr)
+
+
+class W4A16Error(AssertionError, ValueError):
+    """Argument rejected by the library.
+
+    An AssertionError, as the reference's own checks are asserts, and a
+    ValueError for callers that expect one.
+    """
+
+
+class W4A16RuntimeError(RuntimeError):
+    """The HIP runtime reported a failure."""
+
+
+def check(status: int) -> None:
+    if status == W4A16_OK:
+        return
+    msg = f"w4a16_moe: {strerror(status)} (status {status})"
+    if status == W4A16_ERR_HIP:
+        raise W4A16RuntimeError(msg)
+    raise W4A16Error(msg)

@@ -1,0 +1,201 @@
+// Token-to-expert sort with block padding (moe_align_block_size) for gfx950.
+//
+// Reference: kernels/w4a16_moe.py:187-290 builds the same outputs from ~25
+// torch ops (scatter_add_ histogram, cumsum of padded counts, stable sort,
+// scatter_reduce amin for the rank, index_put, searchsorted, masked_fill).
+// Here it is one workgroup and one launch:
+//   1. every wave owns a contiguous chunk of the flat (token, slot) index
+//      range and histograms it into its own LDS row cnt[wave][expert];
+//   2. a column prefix over the wave rows turns cnt into each wave's
+//      starting rank inside every expert (this is what makes the sort stable:
+//      earlier chunks rank first);
+//   3. a workgroup scan of the padded counts gives the expert offsets;
+//   4. every wave walks its chunk again 64 indices at a time; lanes routed to
+//      the same expert find each other with ballots over the expert-id bits,
+//      take rank = popcount(peers below me) and the lowest peer advances the
+//      wave's cursor -- ascending flat index inside an expert, as a stable
+//      sort gives;
+//   5. padding slots and the tail get the sentinel M*topk, blocks get their
+//      expert by binary search of the offsets (searchsorted right=True),
+//      blocks past the padded end get -1.
+// Integer only; the output is bit-identical to the reference over the whole
+// fixed-size buffers.  Ids outside [0, E) are skipped and counted.
+#include "common.hpp"
+
+namespace w4a16 {
+namespace {
+
+// Exclusive scan of one int per thread over the workgroup.
+__device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wave_tot[wid] = x;
+  __syncthreads();
+  if (wid == 0) {
+    const int t = lane < nw ? wave_tot[lane] : 0;
+    int s = t;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(s, d, 64);
+      if (lane >= d) s += y;
+    }
+    if (lane < nw) wave_tot[lane] = s - t;
+    if (lane == nw - 1) wave_tot[16] = s;
+  }
+  __syncthreads();
+  *total = wave_tot[16];
+  const int excl = x - v + wave_tot[wid];
+  __syncthreads();
+  return excl;
+}
+
+__global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
+  extern __shared__ int32_t smem[];
+  __shared__ int32_t wave_tot[17];
+  __shared__ int32_t s_drop;
+
+  const int nthr = blockDim.x;
+  const int nw = nthr >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int E = a.num_experts;
+  const int B = a.block;
+  const int n_tok = a.n_tok;
+
+  int32_t* cnt = smem;           // [nw][E]
+  int32_t* off = cnt + nw * E;   // [E+1]
+  int32_t* tot = off + E + 1;    // [E]
+
+  for (int i = tid; i < nw * E; i += nthr) cnt[i] = 0;
+  if (tid == 0) s_drop = 0;
+  __syncthreads();
+
+  // Contiguous chunk of flat indices per wave, a multiple of 64.
+  const int per = ((n_tok + nw - 1) / nw + 63) & ~63;
+  const int beg = min(n_tok, wid * per);
+  const int end = min(n_tok, beg + per);
+
+  // 1. per-wave histogram
+  int drop = 0;
+  for (int f0 = beg; f0 < end; f0 += 64) {
+    const int f = f0 + lane;
+    if (f < end) {
+      const int e = a.ids[f];
+      if (e >= 0 && e < E)
+        atomicAdd(&cnt[wid * E + e], 1);
+      else
+        ++drop;
+    }
+  }
+  if (drop) atomicAdd(&s_drop, drop);
+  __syncthreads();
+
+  // 2. column prefix over waves: cnt[w][e] <- rank of wave w's first pair
+  for (int e = tid; e < E; e += nthr) {
+    int run = 0;
+    for (int w = 0; w < nw; ++w) {
+      const int c = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+
+  // 3. offsets = exclusive scan of counts rounded up to the block size
+  const int ipt = (E + nthr - 1) / nthr;
+  const int e0 = tid * ipt;
+  int local = 0;
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e < E) local += (tot[e] + B - 1) / B * B;
+  }
+  int total = 0;
+  int excl = block_exclusive_scan(local, wave_tot, &total);
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      off[e] = excl;
+      excl += (tot[e] + B - 1) / B * B;
+    }
+  }
+  if (tid == 0) off[E] = total;
+  __syncthreads();
+  for (int i = tid; i < nw * E; i += nthr) cnt[i] += off[i % E];
+  __syncthreads();
+
+  // 4. stable placement
+  int ebits = 0;
+  while ((1 << ebits) < E) ++ebits;
+  const uint64_t lt = lanemask_lt();
+  for (int f0 = beg; f0 < end; f0 += 64) {
+    const int f = f0 + lane;
+    const int e = f < end ? a.ids[f] : -1;
+    const bool ok = f < end && e >= 0 && e < E;
+    uint64_t peers = ballot(ok);
+    for (int bit = 0; bit < ebits; ++bit) {
+      const bool set = ok && ((e >> bit) & 1);
+      const uint64_t m = ballot(set);
+      peers &= set ? m : ~m;
+    }
+    int base = 0;
+    if (ok) base = cnt[wid * E + e];
+    __builtin_amdgcn_wave_barrier();
+    if (ok) {
+      const uint64_t below = peers & lt;
+      a.sorted[base + __popcll(below)] = f;
+      if (below == 0) cnt[wid * E + e] = base + __popcll(peers);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // 5. sentinels, expert ids, scalars
+  for (int e = tid; e < E; e += nthr) {
+    const int p1 = off[e + 1];
+    for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
+  }
+  for (int p = total + tid; p < a.em; p += nthr) a.sorted[p] = n_tok;
+  for (int b = tid; b < a.n_blocks; b += nthr) {
+    int eid = -1;
+    const int pos = b * B;
+    if (pos < total) {
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid + 1] > pos)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      eid = lo;
+    }
+    a.expert_ids[b] = eid;
+  }
+  if (a.offsets)
+    for (int e = tid; e <= E; e += nthr) a.offsets[e] = off[e];
+  if (tid == 0) {
+    a.num_post[0] = total;
+    if (a.dropped) a.dropped[0] = s_drop;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_align(const AlignLaunch& a, hipStream_t stream) {
+  const int threads = a.num_experts <= 512 ? 1024 : 512;
+  const int nw = threads / 64;
+  const size_t lds =
+      sizeof(int32_t) * ((size_t)nw * a.num_experts + 2 * (size_t)a.num_experts + 1);
+  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(threads), lds, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace w4a16

@@ -1,0 +1,324 @@
+// C ABI of the W4A16 MoE library: argument checks, workspace layout and the
+// launch sequence align -> w13 -> w2 -> combine, all on the caller's stream.
+#include <limits.h>
+
+#include "../../include/w4a16_moe.h"
+#include "common.hpp"
+
+using namespace w4a16;
+
+namespace {
+
+constexpr size_t kWsAlign = 256;
+constexpr int64_t kMaxExperts = 1024;
+constexpr int64_t kMaxTopk = 256;
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int align_sizes(int64_t M, int64_t topk, int64_t E, int64_t block, int64_t* em,
+                int64_t* nb) {
+  if (block < 1) return W4A16_ERR_INVALID_BLOCK;
+  if (M < 0 || topk < 1 || E < 1) return W4A16_ERR_INVALID_SHAPE;
+  if (topk > kMaxTopk || E > kMaxExperts) return W4A16_ERR_INVALID_SHAPE;
+  if (block > (int64_t)INT_MAX / (kMaxExperts + 1)) return W4A16_ERR_INVALID_BLOCK;
+  const int64_t n_tok = M * topk;
+  const int64_t padded = n_tok + E * (block - 1);
+  const int64_t e_m = (padded + block - 1) / block * block;
+  if (n_tok > INT_MAX / 2 || e_m > INT_MAX / 2) return W4A16_ERR_INVALID_SHAPE;
+  *em = e_m;
+  *nb = e_m / block;
+  return W4A16_OK;
+}
+
+struct Layout {
+  size_t off[W4A16_WS_NFIELDS];
+  size_t total;
+  int64_t em, nb;
+};
+
+int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
+  if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
+  if (group != 32 && group != 64 && group != 128) return W4A16_ERR_UNSUPPORTED_GROUP;
+  if (K % group != 0 || N % group != 0) return W4A16_ERR_UNSUPPORTED_GROUP;
+  if (K % 32 != 0 || N % 32 != 0) return W4A16_ERR_INVALID_SHAPE;
+  // one staged activation row (K or N bf16 values) must fit in LDS
+  if (K > 16384 || N > 16384) return W4A16_ERR_INVALID_SHAPE;
+  return W4A16_OK;
+}
+
+int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
+                   int64_t group, Layout* L) {
+  int st = check_gemm_shape(N, K, group);
+  if (st) return st;
+  st = align_sizes(M, topk, E, W4A16_FUSED_BLOCK_M, &L->em, &L->nb);
+  if (st) return st;
+  const size_t n_tok = (size_t)(M * topk);
+  size_t cur = 0;
+  auto put = [&](int field, size_t bytes) {
+    L->off[field] = cur;
+    cur = round_up(cur + bytes, kWsAlign);
+  };
+  put(W4A16_WS_HEADER, 64 * sizeof(int32_t));
+  put(W4A16_WS_SORTED_IDS, (size_t)L->em * sizeof(int32_t));
+  put(W4A16_WS_EXPERT_IDS, (size_t)L->nb * sizeof(int32_t));
+  put(W4A16_WS_OFFSETS, (size_t)(E + 1) * sizeof(int32_t));
+  put(W4A16_WS_INTER, n_tok * (size_t)N * sizeof(uint16_t));
+  put(W4A16_WS_PARTIAL, n_tok * (size_t)K * sizeof(float));
+  L->total = cur;
+  return W4A16_OK;
+}
+
+bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+struct FusedArgs {
+  const void* hidden;
+  int64_t ld_hidden;
+  const void* w13;
+  const void* w2;
+  const void* s13;
+  const void* s2;
+  const float* topk_w;
+  const int32_t* ids;
+  int64_t M, topk, E, N, K, group;
+  void* out;
+  int64_t ld_out;
+  void* ws;
+  size_t ws_bytes;
+};
+
+int validate(const FusedArgs& a, Layout* L) {
+  int st = compute_layout(a.M, a.topk, a.E, a.N, a.K, a.group, L);
+  if (st) return st;
+  if (a.M == 0) return W4A16_OK;
+  if (!a.hidden || !a.w13 || !a.w2 || !a.s13 || !a.s2 || !a.topk_w || !a.ids ||
+      !a.out || !a.ws)
+    return W4A16_ERR_NULL_POINTER;
+  if (a.ld_hidden < a.K || a.ld_out < a.K) return W4A16_ERR_INVALID_SHAPE;
+  if (a.ws_bytes < L->total) return W4A16_ERR_WORKSPACE_TOO_SMALL;
+  if (!aligned(a.hidden, 16) || a.ld_hidden % 8 != 0) return W4A16_ERR_MISALIGNED;
+  if (!aligned(a.w13, 16) || !aligned(a.w2, 16)) return W4A16_ERR_MISALIGNED;
+  if (!aligned(a.s13, 2) || !aligned(a.s2, 2) || !aligned(a.out, 2))
+    return W4A16_ERR_MISALIGNED;
+  if (!aligned(a.topk_w, 4) || !aligned(a.ids, 4) || !aligned(a.ws, kWsAlign))
+    return W4A16_ERR_MISALIGNED;
+  return W4A16_OK;
+}
+
+// Launch the four stages; `ev` (5 events or null) brackets them.
+int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_t* ev) {
+  char* ws = static_cast<char*>(a.ws);
+  int32_t* header = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_HEADER]);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_SORTED_IDS]);
+  int32_t* eids = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_EXPERT_IDS]);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_OFFSETS]);
+  uint16_t* inter = reinterpret_cast<uint16_t*>(ws + L.off[W4A16_WS_INTER]);
+  float* partial = reinterpret_cast<float*>(ws + L.off[W4A16_WS_PARTIAL]);
+  const int32_t n_tok = (int32_t)(a.M * a.topk);
+
+  (void)hipGetLastError();
+  if (ev && hipEventRecord(ev[0], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  AlignLaunch al;
+  al.ids = a.ids;
+  al.n_tok = n_tok;
+  al.num_experts = (int32_t)a.E;
+  al.block = W4A16_FUSED_BLOCK_M;
+  al.em = (int32_t)L.em;
+  al.n_blocks = (int32_t)L.nb;
+  al.sorted = sorted;
+  al.expert_ids = eids;
+  al.num_post = header;
+  al.offsets = offsets;
+  al.dropped = header + 1;
+  if (launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  GemvLaunch g;
+  g.sorted = sorted;
+  g.expert_ids = eids;
+  g.header = header;
+  g.n_tok = n_tok;
+  g.topk = (int32_t)a.topk;
+  g.block = W4A16_FUSED_BLOCK_M;
+  g.group = (int32_t)a.group;
+  g.max_blocks = (int32_t)(L.nb < n_tok ? L.nb : n_tok);
+  g.num_experts = (int32_t)a.E;
+
+  g.act = static_cast<const uint16_t*>(a.hidden);
+  g.ld_act = a.ld_hidden;
+  g.w = static_cast<const uint32_t*>(a.w13);
+  g.s = static_cast<const uint16_t*>(a.s13);
+  g.topk_w = nullptr;
+  g.out = inter;
+  g.n_out = (int32_t)a.N;
+  g.kdim = (int32_t)a.K;
+  if (launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (ev && hipEventRecord(ev[2], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  g.act = inter;
+  g.ld_act = a.N;
+  g.w = static_cast<const uint32_t*>(a.w2);
+  g.s = static_cast<const uint16_t*>(a.s2);
+  g.topk_w = a.topk_w;
+  g.out = partial;
+  g.n_out = (int32_t)a.K;
+  g.kdim = (int32_t)a.N;
+  if (launch_w2_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (ev && hipEventRecord(ev[3], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  CombineLaunch c;
+  c.partial = partial;
+  c.ids = a.ids;
+  c.out = static_cast<uint16_t*>(a.out);
+  c.ld_out = a.ld_out;
+  c.M = (int32_t)a.M;
+  c.topk = (int32_t)a.topk;
+  c.K = (int32_t)a.K;
+  c.num_experts = (int32_t)a.E;
+  if (launch_combine(c, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (ev && hipEventRecord(ev[4], stream) != hipSuccess) return W4A16_ERR_HIP;
+  return W4A16_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int w4a16_moe_abi_version(void) { return 1; }
+
+const char* w4a16_moe_strerror(int status) {
+  switch (status) {
+    case W4A16_OK: return "ok";
+    case W4A16_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case W4A16_ERR_INVALID_SHAPE: return "invalid or unsupported shape";
+    case W4A16_ERR_UNSUPPORTED_GROUP:
+      return "group_size must be 32, 64 or 128 and divide K and N";
+    case W4A16_ERR_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case W4A16_ERR_MISALIGNED: return "pointer or row stride misaligned";
+    case W4A16_ERR_INVALID_BLOCK: return "invalid block_size";
+    case W4A16_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int w4a16_moe_align_sizes(int64_t M, int64_t topk, int64_t num_experts,
+                          int64_t block_size, int64_t* max_num_tokens_padded,
+                          int64_t* max_num_m_blocks) {
+  if (!max_num_tokens_padded || !max_num_m_blocks) return W4A16_ERR_NULL_POINTER;
+  return align_sizes(M, topk, num_experts, block_size, max_num_tokens_padded,
+                     max_num_m_blocks);
+}
+
+int w4a16_moe_align_block_size(const int32_t* topk_ids, int64_t M, int64_t topk,
+                               int64_t num_experts, int64_t block_size,
+                               int32_t* sorted_token_ids, int32_t* expert_ids,
+                               int32_t* num_tokens_post_padded,
+                               int32_t* expert_offsets, int32_t* dropped,
+                               void* stream) {
+  int64_t em = 0, nb = 0;
+  const int st = align_sizes(M, topk, num_experts, block_size, &em, &nb);
+  if (st) return st;
+  if ((M > 0 && !topk_ids) || !sorted_token_ids || !expert_ids || !num_tokens_post_padded)
+    return W4A16_ERR_NULL_POINTER;
+  AlignLaunch al;
+  al.ids = topk_ids;
+  al.n_tok = (int32_t)(M * topk);
+  al.num_experts = (int32_t)num_experts;
+  al.block = (int32_t)block_size;
+  al.em = (int32_t)em;
+  al.n_blocks = (int32_t)nb;
+  al.sorted = sorted_token_ids;
+  al.expert_ids = expert_ids;
+  al.num_post = num_tokens_post_padded;
+  al.offsets = expert_offsets;
+  al.dropped = dropped;
+  (void)hipGetLastError();
+  return launch_align(al, static_cast<hipStream_t>(stream)) == hipSuccess ? W4A16_OK
+                                                                         : W4A16_ERR_HIP;
+}
+
+int w4a16_moe_workspace_size(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                             int64_t K, int64_t group_size, size_t* bytes) {
+  if (!bytes) return W4A16_ERR_NULL_POINTER;
+  Layout L;
+  const int st = compute_layout(M, topk, num_experts, N, K, group_size, &L);
+  if (st) return st;
+  *bytes = L.total;
+  return W4A16_OK;
+}
+
+int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                               int64_t K, int64_t group_size,
+                               size_t offsets[W4A16_WS_NFIELDS]) {
+  if (!offsets) return W4A16_ERR_NULL_POINTER;
+  Layout L;
+  const int st = compute_layout(M, topk, num_experts, N, K, group_size, &L);
+  if (st) return st;
+  for (int i = 0; i < W4A16_WS_NFIELDS; ++i) offsets[i] = L.off[i];
+  return W4A16_OK;
+}
+
+int w4a16_moe_fused_experts(const void* hidden, int64_t ld_hidden, const void* w13_packed,
+                            const void* w2_packed, const void* w13_scale,
+                            const void* w2_scale, const float* topk_weights,
+                            const int32_t* topk_ids, int64_t M, int64_t topk,
+                            int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
+                            void* out, int64_t ld_out, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
+                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
+                    out, ld_out, workspace, workspace_bytes};
+  Layout L;
+  const int st = validate(a, &L);
+  if (st || M == 0) return st;
+  return run_fused(a, L, static_cast<hipStream_t>(stream), nullptr);
+}
+
+int w4a16_moe_fused_experts_profiled(
+    const void* hidden, int64_t ld_hidden, const void* w13_packed, const void* w2_packed,
+    const void* w13_scale, const void* w2_scale, const float* topk_weights,
+    const int32_t* topk_ids, int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+    int64_t K, int64_t group_size, void* out, int64_t ld_out, void* workspace,
+    size_t workspace_bytes, void* stream, float stage_ms[4]) {
+  if (!stage_ms) return W4A16_ERR_NULL_POINTER;
+  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
+                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
+                    out, ld_out, workspace, workspace_bytes};
+  Layout L;
+  int st = validate(a, &L);
+  if (st) return st;
+  for (int i = 0; i < 4; ++i) stage_ms[i] = 0.0f;
+  if (M == 0) return W4A16_OK;
+  hipEvent_t ev[5];
+  int made = 0;
+  for (; made < 5; ++made)
+    if (hipEventCreate(&ev[made]) != hipSuccess) break;
+  if (made < 5) {
+    for (int i = 0; i < made; ++i) (void)hipEventDestroy(ev[i]);
+    return W4A16_ERR_HIP;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  st = run_fused(a, L, s, ev);
+  if (st == W4A16_OK && hipEventSynchronize(ev[4]) != hipSuccess) st = W4A16_ERR_HIP;
+  if (st == W4A16_OK) {
+    for (int i = 0; i < 4; ++i) {
+      float ms = 0.0f;
+      if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) != hipSuccess) st = W4A16_ERR_HIP;
+      stage_ms[i] = ms;
+    }
+  }
+  for (int i = 0; i < 5; ++i) (void)hipEventDestroy(ev[i]);
+  return st;
+}
+
+int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count, void* stream) {
+  if (!workspace || !count) return W4A16_ERR_NULL_POINTER;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t* header = static_cast<const int32_t*>(workspace);  // header is field 0
+  if (hipMemcpyAsync(count, header + 1, sizeof(int32_t), hipMemcpyDeviceToHost, s) !=
+      hipSuccess)
+    return W4A16_ERR_HIP;
+  return hipStreamSynchronize(s) == hipSuccess ? W4A16_OK : W4A16_ERR_HIP;
+}
+
+}  // extern "C"

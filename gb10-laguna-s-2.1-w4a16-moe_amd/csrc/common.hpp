@@ -1,0 +1,114 @@
+// Shared device helpers and the host-side launcher declarations of the
+// W4A16 MoE library (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace w4a16 {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (hardware conversion on gfx950).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  __bf16 h = (__bf16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// DPP lane moves on 32-bit values.  All controls used here read a valid lane
+// for every destination lane.
+//   0xB1  quad_perm [1,0,3,2]  (lane ^ 1)
+//   0x4E  quad_perm [2,3,0,1]  (lane ^ 2)
+//   0x141 row_half_mirror      (lane i <- lane 7-i within 8 lanes)
+//   0x140 row_mirror           (lane i <- lane 15-i within 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of 4 lanes; every lane of the quad gets the sum.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  return v;
+}
+
+// Sum over aligned groups of 8 lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float oct_sum(float v) {
+  v = quad_sum(v);
+  v += dpp_f32<0x141>(v);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) {
+  return __builtin_amdgcn_ballot_w64(p);
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const uint32_t lane = __lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+}  // namespace w4a16
+
+// ---- host launchers (defined next to their kernels) ----------------------
+namespace w4a16 {
+
+struct AlignLaunch {
+  const int32_t* ids;
+  int32_t n_tok;
+  int32_t num_experts;
+  int32_t block;
+  int32_t em;        // sorted_token_ids length
+  int32_t n_blocks;  // expert_ids length
+  int32_t* sorted;
+  int32_t* expert_ids;
+  int32_t* num_post;
+  int32_t* offsets;  // may be null, [E+1]
+  int32_t* dropped;  // may be null, [1]
+};
+hipError_t launch_align(const AlignLaunch& a, hipStream_t stream);
+
+struct GemvLaunch {
+  const uint16_t* act;     // bf16 activation rows
+  int64_t ld_act;          // row stride (elements)
+  const uint32_t* w;       // packed weights [E, rows_total, kdim/8]
+  const uint16_t* s;       // bf16 scales   [E, rows_total, kdim/G]
+  const int32_t* sorted;
+  const int32_t* expert_ids;
+  const int32_t* header;   // [0] = num_tokens_post_padded
+  const float* topk_w;     // w2 only
+  void* out;               // w13: bf16 inter [n_tok, n_out]; w2: fp32 [n_tok, n_out]
+  int32_t n_tok;
+  int32_t topk;
+  int32_t block;
+  int32_t n_out;           // output rows (N for w13, K for w2)
+  int32_t kdim;            // reduction length (K for w13, N for w2)
+  int32_t group;
+  int32_t max_blocks;      // upper bound of active blocks
+  int32_t num_experts;
+};
+hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
+hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);
+
+struct CombineLaunch {
+  const float* partial;    // [M*topk, K]
+  const int32_t* ids;      // [M, topk]
+  uint16_t* out;           // bf16 [M, ld_out]
+  int64_t ld_out;
+  int32_t M;
+  int32_t topk;
+  int32_t K;
+  int32_t num_experts;
+};
+hipError_t launch_combine(const CombineLaunch& a, hipStream_t stream);
+
+}  // namespace w4a16

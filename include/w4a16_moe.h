@@ -1,0 +1,164 @@
+/*
+ * w4a16_moe.h -- C ABI of the MI355X (gfx950) W4A16 grouped-expert MoE path.
+ *
+ * One MoE layer: out[M,K] = sum_t w[m,t] * W2_e (SiLU(Wg_e x_m) * (Wu_e x_m)),
+ * e = topk_ids[m,t], with int4 weights stored in the compressed-tensors
+ * "pack-quantized" layout, consumed unchanged:
+ *
+ *   w13_packed  [E, 2N, K/8]  int32  (== [E, 2N, K/2] uint8), rows 0..N-1 gate,
+ *                                    rows N..2N-1 up; element k of a row is
+ *                                    nibble (k % 8) of word k/8, value = code-8
+ *   w13_scale   [E, 2N, K/G]  bf16   one symmetric scale per G elements of K
+ *   w2_packed   [E, K,  N/8]  int32
+ *   w2_scale    [E, K,  N/G]  bf16
+ *   hidden      [M, K]        bf16   (row stride ld_hidden elements)
+ *   topk_ids    [M, topk]     int32  contiguous
+ *   topk_weights[M, topk]     fp32   contiguous
+ *   out         [M, K]        bf16   (row stride ld_out elements)
+ *
+ * Contract of every entry point:
+ *   - status 0 (W4A16_OK) on success; argument errors are detected on the
+ *     host before any GPU work is enqueued;
+ *   - all GPU work is enqueued on `stream` (a hipStream_t; NULL = default
+ *     stream) with no host synchronisation and no device allocation, so a
+ *     call can be captured into a HIP graph (the *_profiled variant excepted);
+ *   - the library holds no mutable global state; concurrent calls that share
+ *     one workspace race, calls with distinct workspaces do not;
+ *   - inputs are never modified.
+ *
+ * Expert ids outside [0, E) are not routed: the pair contributes nothing to
+ * the output and is counted in the workspace's dropped-pair counter
+ * (w4a16_moe_dropped_pairs).  The reference indexes out of bounds instead.
+ */
+#ifndef W4A16_MOE_H
+#define W4A16_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define W4A16_OK                      0
+#define W4A16_ERR_NULL_POINTER        1  /* a required pointer is NULL        */
+#define W4A16_ERR_INVALID_SHAPE       2  /* negative / inconsistent / too big */
+#define W4A16_ERR_UNSUPPORTED_GROUP   3  /* group size not 32, 64 or 128 ...   */
+#define W4A16_ERR_WORKSPACE_TOO_SMALL 4
+#define W4A16_ERR_MISALIGNED          5  /* pointer / row stride alignment    */
+#define W4A16_ERR_INVALID_BLOCK       6  /* block_size < 1                    */
+#define W4A16_ERR_HIP                 7  /* a HIP runtime call failed         */
+
+/* Indices of w4a16_moe_workspace_layout()'s offsets array. */
+#define W4A16_WS_SORTED_IDS   0  /* int32 [EM]            sorted token-slot ids   */
+#define W4A16_WS_EXPERT_IDS   1  /* int32 [EM/16]         expert of each block    */
+#define W4A16_WS_HEADER       2  /* int32 [64]: [0] num_tokens_post_padded,
+                                    [1] dropped pairs, [2..] reserved            */
+#define W4A16_WS_OFFSETS      3  /* int32 [E+1]           padded expert offsets   */
+#define W4A16_WS_INTER        4  /* bf16  [M*topk, N]     SiLU(gate)*up           */
+#define W4A16_WS_PARTIAL      5  /* fp32  [M*topk, K]     weighted w2 products    */
+#define W4A16_WS_NFIELDS      6
+
+/* Token-block size the fused call uses for its internal expert sort. */
+#define W4A16_FUSED_BLOCK_M 16
+
+/*
+ * Sizes of moe_align_block_size's outputs.
+ * Replaces the buffer sizing of _align_workspace,
+ * kernels/w4a16_moe.py:153-157:
+ *   EM = round_up(M*topk + E*(block-1), block),  n_blocks = EM / block.
+ */
+int w4a16_moe_align_sizes(int64_t M, int64_t topk, int64_t num_experts,
+                          int64_t block_size, int64_t* max_num_tokens_padded,
+                          int64_t* max_num_m_blocks);
+
+/*
+ * Sort the M*topk (token, slot) pairs by expert, pad every expert to a
+ * multiple of block_size and emit per-block expert ids.
+ * Replaces moe_align_block_size, kernels/w4a16_moe.py:187-290, with
+ * bit-identical outputs over the whole fixed-size buffers:
+ *   sorted_token_ids[EM]  flat index f = m*topk + t, stable (ascending f)
+ *                         within an expert; padding slots hold M*topk;
+ *   expert_ids[EM/block]  expert of each block, -1 after the padded end;
+ *   num_tokens_post_padded[1].
+ * Optional outputs (may be NULL): expert_offsets[E+1] (exclusive prefix of
+ * padded counts) and dropped[1] (pairs whose id is outside [0, E)).
+ * One kernel launch on `stream`.
+ */
+int w4a16_moe_align_block_size(const int32_t* topk_ids, int64_t M,
+                               int64_t topk, int64_t num_experts,
+                               int64_t block_size, int32_t* sorted_token_ids,
+                               int32_t* expert_ids,
+                               int32_t* num_tokens_post_padded,
+                               int32_t* expert_offsets, int32_t* dropped,
+                               void* stream);
+
+/*
+ * Device scratch needed by w4a16_moe_fused_experts (bytes, 256-aligned).
+ * Replaces the scratch pools _align_workspace / _gemm_workspace,
+ * kernels/w4a16_moe.py:141-184 and :293-316.
+ */
+int w4a16_moe_workspace_size(int64_t M, int64_t topk, int64_t num_experts,
+                             int64_t N, int64_t K, int64_t group_size,
+                             size_t* bytes);
+
+/* Byte offsets of the workspace's fields (W4A16_WS_*), for inspection. */
+int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts,
+                               int64_t N, int64_t K, int64_t group_size,
+                               size_t offsets[W4A16_WS_NFIELDS]);
+
+/*
+ * The fused W4A16 MoE layer.
+ * Replaces fused_experts_w4a16, kernels/w4a16_moe.py:678-909 (expert sort,
+ * w13 dequant-GEMM with SiLU(gate)*up, w2 dequant-GEMM with the top-k
+ * weighted combine).  Weights are the unchanged pack-quantized tensors (no
+ * repack).  Accumulation is fp32; the w13 output is rounded to bf16 as in the
+ * reference; the top-k combine is summed in slot order (deterministic).
+ * Requirements: K and N multiples of 32 and of group_size, at most 16384;
+ * group_size in {32, 64, 128}; 1 <= topk <= 256; 1 <= E <= 1024;
+ * hidden and packed-weight pointers 16-byte aligned; ld_hidden % 8 == 0;
+ * workspace 256-byte aligned and at least w4a16_moe_workspace_size bytes.
+ */
+int w4a16_moe_fused_experts(const void* hidden, int64_t ld_hidden,
+                            const void* w13_packed, const void* w2_packed,
+                            const void* w13_scale, const void* w2_scale,
+                            const float* topk_weights, const int32_t* topk_ids,
+                            int64_t M, int64_t topk, int64_t num_experts,
+                            int64_t N, int64_t K, int64_t group_size,
+                            void* out, int64_t ld_out, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
+ * Same computation as w4a16_moe_fused_experts, with HIP events recorded
+ * between its stages; waits for the stream and writes each stage's device
+ * time in milliseconds to stage_ms[4] = {align, w13, w2, combine}.
+ * Measurement helper: no counterpart in the reference.
+ */
+int w4a16_moe_fused_experts_profiled(
+    const void* hidden, int64_t ld_hidden, const void* w13_packed,
+    const void* w2_packed, const void* w13_scale, const void* w2_scale,
+    const float* topk_weights, const int32_t* topk_ids, int64_t M,
+    int64_t topk, int64_t num_experts, int64_t N, int64_t K,
+    int64_t group_size, void* out, int64_t ld_out, void* workspace,
+    size_t workspace_bytes, void* stream, float stage_ms[4]);
+
+/*
+ * Read the dropped-pair counter the last fused call left in `workspace`
+ * (waits for `stream`).  No counterpart in the reference, which has no range
+ * check on topk_ids.
+ */
+int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
+                            void* stream);
+
+/* Human-readable text of a status code (static storage). */
+const char* w4a16_moe_strerror(int status);
+
+/* ABI version of this header: 1. */
+int w4a16_moe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_MOE_H */

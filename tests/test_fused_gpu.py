@@ -1,0 +1,277 @@
+"""HIP fused W4A16 MoE vs the CPU oracle.
+
+Two oracles are used.  ``tight``: exact dequantized weights and the
+intermediate rounded to bf16 -- the HIP path's own rounding points, so only
+fp32 summation order differs.  ``reference``: the reference's dequant
+reference (bf16-rounded dequantized weights, fp32 intermediate,
+bench/bench_moe.py:277-303) at the north-star bar.
+
+Tolerances (north star: max-abs <= 2e-2 and rel-L2 <= 5e-3 in bf16):
+  * rel-L2 <= 5e-3 against the reference oracle at every size;
+  * max-abs <= 2e-2 at the reference bench's magnitudes (x ~ N(0,1)/10,
+    scales ~ 0.02-0.035), where outputs are O(0.1);
+  * at the benchmark magnitudes (outputs O(6), where bf16 rounding of the
+    output alone is ~0.06 max-abs) max-abs is checked relative to max|ref|;
+  * against the tight oracle: rel-L2 <= 2.5e-3 and at most 2 bf16 ulps.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_MAX = 5e-3
+MAX_ABS_MAX = 2e-2
+
+
+def _make(synth, shape, M, dev, seed=0, skewed=False):
+    w13, w2, s13, s2 = synth.make_weights(shape, dev, seed=seed)
+    x = synth.make_hidden(M, shape.K, dev, seed=seed)
+    tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=seed, skewed=skewed)
+    return w13, w2, s13, s2, x, tw, ti
+
+
+def _ulp_bf16(v: torch.Tensor) -> torch.Tensor:
+    a = v.abs().clamp_min(1e-30)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True):
+    out32 = out.float().cpu()
+    ref = orc.moe_reference(x, w13, w2, s13, s2, tw, ti, group, out_dtype=None)
+    rl2 = orc.rel_l2(out32, ref)
+    mab = orc.max_abs(out32, ref)
+    scale = float(ref.abs().max()) + 1e-30
+    msg = f"{tag}: rel_l2={rl2:.3e} max_abs={mab:.3e} max|ref|={scale:.3e}"
+    print(msg, flush=True)
+    assert rl2 <= REL_L2_MAX, msg
+    assert mab <= 2e-2 * scale, msg
+    if tight:
+        t = orc.moe_reference(x, w13, w2, s13, s2, tw, ti, group, exact_weights=True,
+                              round_inter=True, out_dtype=None)
+        trl2 = orc.rel_l2(out32, t)
+        ulps = ((out32 - t).abs() / _ulp_bf16(t)).max().item()
+        print(f"{tag}: tight rel_l2={trl2:.3e} max_ulps={ulps:.2f}", flush=True)
+        assert trl2 <= 2.5e-3, f"{tag}: tight rel_l2 {trl2}"
+        assert ulps <= 2.0, f"{tag}: {ulps} bf16 ulps from the tight oracle"
+    return rl2, mab
+
+
+SMALL = [
+    # E, topk, K, N, group, M
+    (8, 2, 256, 256, 32, 1),
+    (8, 2, 256, 256, 32, 3),
+    (16, 4, 512, 256, 32, 5),
+    (16, 4, 512, 256, 32, 17),
+    (32, 8, 1024, 512, 32, 33),
+    (16, 4, 512, 256, 64, 7),
+    (16, 4, 512, 512, 128, 9),
+    (4, 4, 256, 256, 32, 40),   # every expert gets many tokens (multi-pass staging)
+    (256, 10, 256, 256, 32, 2),
+]
+
+
+@pytest.mark.parametrize("E,topk,K,N,group,M", SMALL)
+def test_fused_small(pkg, orc, synth, dev, E, topk, K, N, group, M):
+    tag = f"small E={E} topk={topk} K={K} N={N} G={group} M={M}"
+    print(tag, flush=True)
+    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=group)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=M)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group)
+    torch.cuda.synchronize()
+    assert out.shape == (M, K) and out.dtype == torch.bfloat16
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag)
+
+
+def test_intermediate_matches_oracle(pkg, orc, synth, dev):
+    """The w13 stage alone: workspace intermediate vs bf16(SiLU(gate)*up)."""
+    shape = synth.LayerShape(E=16, topk=4, K=512, N=256, group=32)
+    M = 6
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=3)
+    pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    ws, off = pkg.workspace_tensor(x, ti, w13, w2, 32)
+    n_tok = M * shape.topk
+    inter = ws[off[4]: off[4] + n_tok * shape.N * 2].view(torch.bfloat16)
+    inter = inter.view(n_tok, shape.N).float().cpu()
+    W13 = orc.dequant_t(w13.cpu(), s13.cpu(), 32, exact=True)
+    xf = x.float().cpu()
+    ids = ti.cpu().reshape(-1)
+    want = torch.empty(n_tok, shape.N)
+    for f in range(n_tok):
+        y = W13[int(ids[f])] @ xf[f // shape.topk]
+        want[f] = (torch.nn.functional.silu(y[: shape.N]) * y[shape.N:])
+    ulps = ((inter - want).abs() / _ulp_bf16(want)).max().item()
+    print(f"intermediate max_ulps={ulps:.3f}", flush=True)
+    assert ulps <= 1.0
+
+
+def test_internal_sort_matches_oracle(pkg, orc, synth, dev):
+    shape = synth.LayerShape(E=64, topk=6, K=256, N=256, group=32)
+    M = 37
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=9)
+    pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    ws, off = pkg.workspace_tensor(x, ti, w13, w2, 32)
+    want = orc.moe_align_block_size(ti.cpu().numpy(), 16, shape.E)
+    em, nb = want[0].size, want[1].size
+    got_s = ws[off[0]: off[0] + 4 * em].view(torch.int32).cpu().numpy()
+    got_e = ws[off[1]: off[1] + 4 * nb].view(torch.int32).cpu().numpy()
+    hdr = ws[off[2]: off[2] + 8].view(torch.int32).cpu().numpy()
+    assert np.array_equal(got_s, want[0])
+    assert np.array_equal(got_e, want[1])
+    assert hdr[0] == want[2][0] and hdr[1] == 0
+
+
+def test_deterministic(pkg, synth, dev):
+    shape = synth.LayerShape(E=32, topk=8, K=512, N=256, group=32)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, 3, dev, seed=1)
+    a = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    x2 = synth.make_hidden(3, shape.K, dev, seed=99)
+    pkg.fused_experts_w4a16(x2, w13, w2, s13, s2, tw, ti, 32)  # dirty the workspace
+    b = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_out_of_range_ids_dropped(pkg, orc, synth, dev):
+    shape = synth.LayerShape(E=16, topk=4, K=256, N=256, group=32)
+    M = 8
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=4)
+    ti = ti.clone()
+    ti[1, 2] = -1
+    ti[5, 0] = shape.E
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    assert pkg.dropped_pairs(x, ti, w13, w2, 32) == 2
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "out-of-range ids")
+
+
+def test_duplicate_ids_in_a_row(pkg, orc, synth, dev):
+    shape = synth.LayerShape(E=8, topk=4, K=256, N=256, group=32)
+    M = 5
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=5)
+    ti = torch.tensor([[1, 1, 2, 1], [0, 0, 0, 0], [7, 6, 7, 5], [3, 4, 3, 4],
+                       [2, 2, 2, 3]], dtype=torch.int32, device=dev)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "duplicate ids")
+
+
+def test_dtypes_and_strides(pkg, orc, synth, dev):
+    shape = synth.LayerShape(E=16, topk=4, K=512, N=256, group=32)
+    M = 6
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=6)
+    ref_out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    # uint8 packed views, int64 ids, bf16 routing weights, strided hidden
+    wide = torch.zeros(M, shape.K + 64, dtype=torch.bfloat16, device=dev)
+    wide[:, 32: 32 + shape.K] = x
+    xs = wide[:, 32: 32 + shape.K]
+    out = pkg.fused_experts_w4a16(xs, w13.view(torch.uint8), w2.view(torch.uint8), s13, s2,
+                                  tw, ti.to(torch.int64), 32)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+    out_bf = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw.to(torch.bfloat16), ti, 32)
+    torch.cuda.synchronize()
+    _check(orc, out_bf, x, w13, w2, s13, s2, tw.to(torch.bfloat16).float(), ti, 32,
+           "bf16 routing weights", tight=False)
+
+
+def test_zero_tokens(pkg, synth, dev):
+    shape = synth.LayerShape(E=8, topk=2, K=256, N=256, group=32)
+    w13, w2, s13, s2 = synth.make_weights(shape, dev)
+    x = torch.empty(0, shape.K, dtype=torch.bfloat16, device=dev)
+    ids = torch.empty(0, 2, dtype=torch.int32, device=dev)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, torch.empty(0, 2, device=dev), ids)
+    assert out.shape == (0, shape.K)
+
+
+def test_graph_capture_replay(pkg, synth, dev):
+    shape = synth.LayerShape(E=32, topk=4, K=512, N=256, group=32)
+    M = 4
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=8)
+    eager = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)  # creates workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        gout = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    for i in range(3):
+        gout.zero_()
+        other = synth.make_hidden(M, shape.K, dev, seed=100 + i)
+        pkg.fused_experts_w4a16(other, w13, w2, s13, s2, tw, ti, 32)  # eager work between
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
+
+
+# ---- full-size layer (E=256, top-10, K=3072, N=1024, group 32) --------------
+
+
+@pytest.fixture(scope="module")
+def full_layer(synth, dev):
+    shape = synth.LayerShape()
+    w = synth.make_weights(shape, dev, seed=0)
+    torch.cuda.synchronize()
+    cpu = tuple(t.cpu() for t in w)
+    yield shape, w, cpu
+    del w
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("cfg_index", [0, 1, 2])
+def test_full_size_decode_configs(pkg, orc, synth, dev, full_layer, cfg_index):
+    shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
+    cfg = synth.CONFIGS[cfg_index]
+    print(f"full-size config {cfg_index}: {cfg.description}", flush=True)
+    x = synth.make_hidden(cfg.M, shape.K, dev, seed=0)
+    tw, ti = synth.make_routing(cfg.M, shape.E, shape.topk, dev, seed=0, skewed=cfg.skewed)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    _check(orc, out, x.cpu(), c13, c2, cs13, cs2, tw.cpu(), ti.cpu(), 32,
+           f"config {cfg_index}", tight=cfg.M <= 16)
+
+
+@pytest.mark.parametrize("cfg_index", [3, 4])
+def test_full_size_prefill_configs_token_sample(pkg, orc, synth, dev, full_layer, cfg_index):
+    """Rows of the output are independent per token: check a sample of them."""
+    shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
+    cfg = synth.CONFIGS[cfg_index]
+    print(f"full-size config {cfg_index}: {cfg.description}", flush=True)
+    x = synth.make_hidden(cfg.M, shape.K, dev, seed=0)
+    tw, ti = synth.make_routing(cfg.M, shape.E, shape.topk, dev, seed=0)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    rows = torch.from_numpy(np.random.default_rng(cfg_index).choice(cfg.M, 12, replace=False))
+    _check(orc, out.cpu()[rows], x.cpu()[rows], c13, c2, cs13, cs2, tw.cpu()[rows],
+           ti.cpu()[rows], 32, f"config {cfg_index} sample", tight=False)
+
+
+def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
+    """max-abs <= 2e-2 at the reference bench's magnitudes (x/10, w ~ randn/10)."""
+    shape = synth.LayerShape()
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    E, K, N = shape.E, shape.K, shape.N
+    w13 = torch.randint(0, 256, (E, 2 * N, K // 2), generator=g, device=dev,
+                        dtype=torch.uint8)
+    w2 = torch.randint(0, 256, (E, K, N // 2), generator=g, device=dev, dtype=torch.uint8)
+    s13 = (torch.rand((E, 2 * N, K // 32), generator=g, device=dev) * 0.015 + 0.02
+           ).to(torch.bfloat16)
+    s2 = (torch.rand((E, K, N // 32), generator=g, device=dev) * 0.015 + 0.02
+          ).to(torch.bfloat16)
+    x = synth.make_hidden(16, K, dev, seed=0, scale=0.1)
+    tw, ti = synth.make_routing(16, E, 10, dev, seed=0)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    rl2, mab = _check(orc, out, x.cpu(), w13.cpu(), w2.cpu(), s13.cpu(), s2.cpu(),
+                      tw.cpu(), ti.cpu(), 32, "reference magnitudes")
+    assert mab <= MAX_ABS_MAX
