@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W4A16 grouped-expert MoE layer.
+
+Metric: weight-bandwidth GB/s = touched-expert packed weight +
+scale bytes / time per call (the reference's definition,
+bench/bench_moe.py:250-263, :742-744), as a fraction of the 8 TB/s HBM peak;
+TFLOP/s = 2*M*topk*(2*N*K + K*N) / time at the prefill sizes.
+
+One "step" is one fused_experts_w4a16 call (sort, w13+SiLU*up, w2, combine)
+on one batch of synthetic input already resident in HBM.  The workload of the
+headline value is BASELINE.json's configs[1]: E=256, top-10, K=3072, N=1024,
+group 32, M=16 tokens, uniform routing.  The other configurations are reported
+in "configs".
+
+Timing: the calls are captured in a HIP graph that cycles through several
+routing/hidden sets (so the touched weights exceed the 256 MB Infinity Cache
+several times over); W warmup calls, then exactly K timed calls bracketed by
+device synchronisation and events on the capturing stream.
+
+Per-kernel durations come from replaying graphs of one stage at a time
+(w4a16_moe_run_stage) over the same sets, timed with events on the stream the
+kernels run on; the dominant kernel's algorithmic bytes / duration is the
+roofline "achieved" figure.
+
+The CPU baseline is the oracle's PyTorch dequant reference
+(oracle/moe_oracle.py, a restatement of bench/bench_moe.py:277-303) timed on
+the host on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]
+                       [--no-sweep] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+METRIC = "weight-BW GB/s (% of HBM peak) at M=1..1024; bf16 TFLOP/s at M=4096 prefill"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+MALL_BYTES = 256 * 2**20       # Infinity Cache
+# The reference's published number for this metric at configs[1] (M=16):
+# 226.3 GB/s on NVIDIA GB10 (results/showdown2.json:1104; README.md:62-70).
+REFERENCE_GBS_M16 = 226.3
+STAGES = ("align", "w13", "w2", "combine")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """One configuration: weights shared, n_sets routing/hidden sets."""
+
+    def __init__(self, pkg, synth, shape, weights, cfg, dev, n_sets=None):
+        import torch
+
+        self.pkg, self.shape, self.cfg, self.dev = pkg, shape, cfg, dev
+        self.w13, self.w2, self.s13, self.s2 = weights
+        M, E = cfg.M, shape.E
+        expect = min(E, M * shape.topk) * shape.bytes_per_expert
+        if n_sets is None:
+            n_sets = min(64, max(8, math.ceil(4 * MALL_BYTES / expect)))
+        self.sets = []
+        for i in range(n_sets):
+            x = synth.make_hidden(M, shape.K, dev, seed=i)
+            tw, ti = synth.make_routing(M, E, shape.topk, dev, seed=i, skewed=cfg.skewed,
+                                        bias_seed=0)
+            self.sets.append((x, tw, ti))
+        self.touched = [synth.touched_experts(s[2], E) for s in self.sets]
+        self.bytes = [n * shape.bytes_per_expert for n in self.touched]
+        self.w13_bytes = [n * shape.w13_bytes_per_expert for n in self.touched]
+        self.w2_bytes = [n * shape.w2_bytes_per_expert for n in self.touched]
+        torch.cuda.synchronize()
+
+    def call(self, i):
+        x, tw, ti = self.sets[i]
+        return self.pkg.fused_experts_w4a16(x, self.w13, self.w2, self.s13, self.s2, tw, ti,
+                                            self.shape.group)
+
+    # ---- whole-call timing (the headline) ----------------------------------
+    def time_calls(self, steps, warmup):
+        import torch
+
+        n = len(self.sets)
+        for j in range(warmup):
+            self.call(j % n)
+        torch.cuda.synchronize()
+        full, rem = divmod(steps, n)
+        graphs = []
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for i in range(n):
+                self.call(i)
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        g_all = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_all):
+            for i in range(n):
+                self.call(i)
+        graphs.append(g_all)
+        g_rem = None
+        if rem:
+            g_rem = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g_rem):
+                for i in range(rem):
+                    self.call(i)
+        # one untimed replay so first-replay costs stay out of the timed region
+        g_all.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(full):
+            g_all.replay()
+        if g_rem is not None:
+            g_rem.replay()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = start.elapsed_time(end)
+        nbytes = full * sum(self.bytes) + sum(self.bytes[:rem])
+        return {"elapsed_ms": ms, "wall_s": wall, "steps": steps, "bytes": nbytes}
+
+    # ---- per-stage timing ---------------------------------------------------
+    def time_stages(self, replays):
+        """Average device time per launch of each stage, over all sets."""
+        import torch
+
+        lib = self.pkg._lib.lib()
+        L = self.pkg._lib
+        shape, M = self.shape, self.cfg.M
+        ws_bytes = L.workspace_size(M, shape.topk, shape.E, shape.N, shape.K, shape.group)
+        wss = [torch.empty(ws_bytes, dtype=torch.uint8, device=self.dev) for _ in self.sets]
+        outs = [torch.empty(M, shape.K, dtype=torch.bfloat16, device=self.dev)
+                for _ in self.sets]
+
+        def args(i):
+            x, tw, ti = self.sets[i]
+            return (x.data_ptr(), x.stride(0), self.w13.data_ptr(), self.w2.data_ptr(),
+                    self.s13.data_ptr(), self.s2.data_ptr(), tw.data_ptr(), ti.data_ptr(),
+                    M, shape.topk, shape.E, shape.N, shape.K, shape.group,
+                    outs[i].data_ptr(), outs[i].stride(0), wss[i].data_ptr(), ws_bytes,
+                    torch.cuda.current_stream().cuda_stream)
+
+        for i in range(len(self.sets)):
+            L.check(lib.w4a16_moe_fused_experts(*args(i)))
+        torch.cuda.synchronize()
+        result = {}
+        for stage, name in enumerate(STAGES):
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for i in range(len(self.sets)):
+                    L.check(lib.w4a16_moe_run_stage(stage, *args(i)))
+            torch.cuda.current_stream().wait_stream(s)
+            with torch.cuda.graph(g):
+                for i in range(len(self.sets)):
+                    L.check(lib.w4a16_moe_run_stage(stage, *args(i)))
+            g.replay()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(replays):
+                g.replay()
+            end.record()
+            torch.cuda.synchronize()
+            result[name] = start.elapsed_time(end) / (replays * len(self.sets))
+        del wss, outs
+        return result
+
+
+def summarize(wl, t, stages):
+    shape, M = wl.shape, wl.cfg.M
+    sec = t["elapsed_ms"] * 1e-3
+    gbs = t["bytes"] / sec / 1e9
+    tflops = shape.flops(M) * t["steps"] / sec / 1e12
+    avg_touched = sum(wl.touched) / len(wl.touched)
+    row = {
+        "config": wl.cfg.index,
+        "M": M,
+        "routing": "skewed" if wl.cfg.skewed else "uniform",
+        "sets": len(wl.sets),
+        "touched_experts_avg": round(avg_touched, 2),
+        "us_per_call": round(t["elapsed_ms"] * 1e3 / t["steps"], 3),
+        "GB_s": round(gbs, 2),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "TFLOP_s": round(tflops, 3),
+        "pct_bf16_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 3),
+    }
+    if stages is not None:
+        row["stage_us"] = {k: round(v * 1e3, 3) for k, v in stages.items()}
+        w13 = sum(wl.w13_bytes) / len(wl.w13_bytes)
+        w2 = sum(wl.w2_bytes) / len(wl.w2_bytes)
+        row["stage_GB_s"] = {"w13": round(w13 / (stages["w13"] * 1e-3) / 1e9, 2),
+                             "w2": round(w2 / (stages["w2"] * 1e-3) / 1e9, 2)}
+    return row
+
+
+def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
+    """Time the oracle's CPU dequant reference on set 0 of the workload."""
+    import torch
+
+    from oracle import moe_oracle as orc
+
+    threads = torch.get_num_threads()
+    x, tw, ti = (t.cpu() for t in wl.sets[0])
+    w = tuple(t.cpu() for t in (wl.w13, wl.w2, wl.s13, wl.s2))
+    gpu_out = wl.call(0).float().cpu()
+    t0 = time.perf_counter()
+    ref = orc.moe_reference(x, *w, tw, ti, wl.shape.group)  # warmup
+    times = [time.perf_counter() - t0]
+    while len(times) < max_iters and sum(times[1:]) < seconds_target:
+        t0 = time.perf_counter()
+        ref = orc.moe_reference(x, *w, tw, ti, wl.shape.group)
+        times.append(time.perf_counter() - t0)
+    timed = sorted(times[1:]) if len(times) > 1 else times
+    p50 = timed[len(timed) // 2]
+    nbytes = wl.bytes[0]
+    ref32 = orc.moe_reference(x, *w, tw, ti, wl.shape.group, out_dtype=None)
+    return {
+        "value": round(nbytes / p50 / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle.moe_reference (PyTorch CPU dequant reference) on routing set 0 of "
+                   f"config {wl.cfg.index} (M={wl.cfg.M}, {wl.touched[0]} touched experts), "
+                   f"1 warmup + {len(timed)} timed calls, p50 {p50 * 1e3:.1f} ms"),
+        "cpu": platform.processor() or platform.machine(),
+        "gpu_vs_cpu_rel_l2": orc.rel_l2(gpu_out, ref32),
+        "gpu_vs_cpu_max_abs": orc.max_abs(gpu_out, ref32),
+    }
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=256)
+    p.add_argument("--warmup", type=int, default=16)
+    p.add_argument("--config", type=int, default=1, help="headline config index (0-4)")
+    p.add_argument("--sets", type=int, default=None, help="routing sets to cycle through")
+    p.add_argument("--no-sweep", action="store_true", help="skip the other configs")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--stage-replays", type=int, default=8)
+    args = p.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        return 2
+    if os.environ.get("WORLD_SIZE", "1") not in ("", "1"):
+        print("bench.py is single-process, single-GPU", file=sys.stderr)
+        return 2
+
+    import torch
+
+    pkg = __graft_entry__.load_package()
+    synth = importlib.import_module(__graft_entry__.PKG_NAME + ".synth")
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    shape = synth.LayerShape()
+    log(f"device {torch.cuda.get_device_name(0)}; generating weights "
+        f"({shape.E * shape.bytes_per_expert / 1e9:.2f} GB)")
+    weights = synth.make_weights(shape, dev, seed=0)
+    torch.cuda.synchronize()
+
+    head_cfg = synth.CONFIGS[args.config]
+    wl = Workload(pkg, synth, shape, weights, head_cfg, dev, n_sets=args.sets)
+    log(f"config {head_cfg.index} ({head_cfg.description}): {len(wl.sets)} sets, "
+        f"avg touched experts {sum(wl.touched) / len(wl.touched):.1f}")
+    t = wl.time_calls(args.steps, args.warmup)
+    log(f"timed {t['steps']} steps in {t['elapsed_ms']:.3f} ms (wall {t['wall_s']:.3f} s)")
+    stages = wl.time_stages(args.stage_replays)
+    head = summarize(wl, t, stages)
+    log(f"headline: {json.dumps(head)}")
+
+    dominant = "w13" if stages["w13"] >= stages["w2"] else "w2"
+    dom_bytes = sum(getattr(wl, f"{dominant}_bytes")) / len(wl.sets)
+    achieved = dom_bytes / (stages[dominant] * 1e-3) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "kernel": f"{dominant} dequant-GEMV (gemv_kernel)",
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "avg_launch_us": round(stages[dominant] * 1e3, 3),
+        "algorithmic_bytes_per_launch": int(dom_bytes),
+    }
+
+    sweep = []
+    if not args.no_sweep:
+        for cfg in synth.CONFIGS:
+            if cfg.index == head_cfg.index:
+                sweep.append(head)
+                continue
+            w = Workload(pkg, synth, shape, weights, cfg, dev)
+            steps = len(w.sets) * (4 if cfg.M <= 64 else 2)
+            tt = w.time_calls(steps, min(8, len(w.sets)))
+            st = w.time_stages(2)
+            row = summarize(w, tt, st)
+            log(f"config {cfg.index}: {json.dumps(row)}")
+            sweep.append(row)
+            del w
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline ...")
+        cpu = cpu_baseline(wl)
+        log(f"cpu baseline: {json.dumps(cpu)}")
+
+    sec = t["elapsed_ms"] * 1e-3
+    value = t["bytes"] / sec / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": t["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(t["elapsed_ms"] / t["steps"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REFERENCE_GBS_M16, 3) if head_cfg.index == 1 else None,
+        "baseline_ref": "reference kernel, GB10, M=16: 226.3 GB/s (results/showdown2.json:1104)",
+        "dtype": "bf16",
+        "data": ("synthetic: int4 codes uniform, bf16 scales U[0.005,0.02], x ~ N(0,1) bf16, "
+                 "router logits N(0,1) fp32 -> top-10 softmax; routing/hidden sets rotated "
+                 "to defeat the 256 MB Infinity Cache"),
+        "config": {"workload": f"configs[{head_cfg.index}]: {head_cfg.description}; one MoE "
+                               "layer E=256 top-10 K=3072 N=1024 group-32",
+                   "M": head_cfg.M, "E": shape.E, "topk": shape.topk, "K": shape.K,
+                   "N": shape.N, "group": shape.group, "sets": len(wl.sets),
+                   "parallelism": "single GPU"},
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "configs": sweep,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "w4a16_moe_workspace_layout",
     "w4a16_moe_fused_experts",
     "w4a16_moe_fused_experts_profiled",
+    "w4a16_moe_run_stage",
     "w4a16_moe_dropped_pairs",
     "w4a16_moe_strerror",
     "w4a16_moe_abi_version",
@@ -80,6 +81,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.w4a16_moe_fused_experts.argtypes = fused
     lib.w4a16_moe_fused_experts_profiled.restype = ctypes.c_int
     lib.w4a16_moe_fused_experts_profiled.argtypes = fused + [ctypes.POINTER(ctypes.c_float)]
+    lib.w4a16_moe_run_stage.restype = ctypes.c_int
+    lib.w4a16_moe_run_stage.argtypes = [ctypes.c_int] + fused
     lib.w4a16_moe_dropped_pairs.restype = ctypes.c_int
     lib.w4a16_moe_dropped_pairs.argtypes = [_vp, ctypes.POINTER(ctypes.c_int32), _vp]
 

@@ -104,8 +104,11 @@ int validate(const FusedArgs& a, Layout* L) {
   return W4A16_OK;
 }
 
-// Launch the four stages; `ev` (5 events or null) brackets them.
-int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_t* ev) {
+// Launch the four stages (or only stage `only` when it is 0..3); `ev`
+// (5 events or null) brackets them.
+int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_t* ev,
+              int only = -1) {
+  auto want = [only](int stage) { return only < 0 || only == stage; };
   char* ws = static_cast<char*>(a.ws);
   int32_t* header = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_HEADER]);
   int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_SORTED_IDS]);
@@ -130,7 +133,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   al.num_post = header;
   al.offsets = offsets;
   al.dropped = header + 1;
-  if (launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(0) && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
 
   GemvLaunch g;
@@ -152,7 +155,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.out = inter;
   g.n_out = (int32_t)a.N;
   g.kdim = (int32_t)a.K;
-  if (launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(1) && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[2], stream) != hipSuccess) return W4A16_ERR_HIP;
 
   g.act = inter;
@@ -163,7 +166,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.out = partial;
   g.n_out = (int32_t)a.K;
   g.kdim = (int32_t)a.N;
-  if (launch_w2_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(2) && launch_w2_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[3], stream) != hipSuccess) return W4A16_ERR_HIP;
 
   CombineLaunch c;
@@ -175,7 +178,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   c.topk = (int32_t)a.topk;
   c.K = (int32_t)a.K;
   c.num_experts = (int32_t)a.E;
-  if (launch_combine(c, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(3) && launch_combine(c, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[4], stream) != hipSuccess) return W4A16_ERR_HIP;
   return W4A16_OK;
 }
@@ -218,7 +221,9 @@ int w4a16_moe_align_block_size(const int32_t* topk_ids, int64_t M, int64_t topk,
   int64_t em = 0, nb = 0;
   const int st = align_sizes(M, topk, num_experts, block_size, &em, &nb);
   if (st) return st;
-  if ((M > 0 && !topk_ids) || !sorted_token_ids || !expert_ids || !num_tokens_post_padded)
+  // zero-length outputs (M = 0 with block 1) may be NULL
+  if ((M > 0 && !topk_ids) || (em > 0 && !sorted_token_ids) || (nb > 0 && !expert_ids) ||
+      !num_tokens_post_padded)
     return W4A16_ERR_NULL_POINTER;
   AlignLaunch al;
   al.ids = topk_ids;
@@ -309,6 +314,23 @@ int w4a16_moe_fused_experts_profiled(
   }
   for (int i = 0; i < 5; ++i) (void)hipEventDestroy(ev[i]);
   return st;
+}
+
+int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
+                        const void* w13_packed, const void* w2_packed,
+                        const void* w13_scale, const void* w2_scale,
+                        const float* topk_weights, const int32_t* topk_ids, int64_t M,
+                        int64_t topk, int64_t num_experts, int64_t N, int64_t K,
+                        int64_t group_size, void* out, int64_t ld_out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (stage < 0 || stage > 3) return W4A16_ERR_INVALID_SHAPE;
+  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
+                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
+                    out, ld_out, workspace, workspace_bytes};
+  Layout L;
+  const int st = validate(a, &L);
+  if (st || M == 0) return st;
+  return run_fused(a, L, static_cast<hipStream_t>(stream), nullptr, stage);
 }
 
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count, void* stream) {

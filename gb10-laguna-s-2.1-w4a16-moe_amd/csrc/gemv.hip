@@ -145,20 +145,20 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
   for (int t0 = 0; t0 < T; t0 += TC) {
     const int tc = min(TC, T - t0);
 
+    // Weight and raw bf16 scale registers of PF steps in flight.  Scales
+    // stay as raw bits until use: converting right after the load would make
+    // the compiler wait for it there and serialise the prefetch ring.
     uint4 wb[PF][NR];
-    float sb[PF][NR];
-    auto load_step = [&](uint4 (&wq)[NR], float (&sq)[NR], int it) {
-      const int gi = it * 8 + sl;
-      const bool in = it < n_it && gi < G;
+    uint32_t sb[PF][NR];
+    // Loads are unconditional so the waitcnt pass sees the same number of
+    // loads in flight on every path: steps past the row end re-read the last
+    // step's lines (cache hits) and their results are never used.
+    auto load_step = [&](uint4 (&wq)[NR], uint32_t (&sq)[NR], int it) {
+      const int gi = min(min(it, n_it - 1) * 8 + sl, G - 1);
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        if (in) {
-          wq[j] = wrow[j][gi];
-          sq[j] = bf16_to_f32(srow[j][gi >> gshift]);
-        } else {
-          wq[j] = make_uint4(0u, 0u, 0u, 0u);
-          sq[j] = 0.0f;
-        }
+        wq[j] = wrow[j][gi];
+        sq[j] = srow[j][gi >> gshift];
       }
     };
 #pragma unroll
@@ -183,10 +183,10 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
 #pragma unroll
       for (int p = 0; p < PF; ++p) {
         const int it = it0 + p;
-        if (it < n_it) {
+        if (it < n_it) {  // wave-uniform; no loads inside
           const int gi = it * 8 + sl;
           const bool in = gi < G;
-          const int gl = in ? gi : 0;
+          const int gl = in ? gi : G - 1;
 #pragma unroll
           for (int t = 0; t < TC; ++t) {
             if (t < tc) {
@@ -199,12 +199,13 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
                 pj = word_dot(wb[p][j].y, x1, pj);
                 pj = word_dot(wb[p][j].z, x2, pj);
                 pj = word_dot(wb[p][j].w, x3, pj);
-                acc[j][t] = fmaf(sb[p][j], pj - c, acc[j][t]);
+                const float sc = in ? bf16_to_f32(sb[p][j]) : 0.0f;
+                acc[j][t] = fmaf(sc, pj - c, acc[j][t]);
               }
             }
           }
-          load_step(wb[p], sb[p], it + PF);
         }
+        load_step(wb[p], sb[p], it + PF);
       }
     }
 

@@ -112,12 +112,17 @@ def make_hidden(M: int, K: int, device, seed: int = 0, scale: float = 1.0) -> to
     return (torch.randn((M, K), generator=g, device=device) * scale).to(torch.bfloat16)
 
 
-def make_routing(M: int, E: int, topk: int, device, seed: int = 0, skewed: bool = False):
-    """(topk_weights fp32 [M, topk], topk_ids int32 [M, topk])."""
+def make_routing(M: int, E: int, topk: int, device, seed: int = 0, skewed: bool = False,
+                 bias_seed: int | None = None):
+    """(topk_weights fp32 [M, topk], topk_ids int32 [M, topk]).
+
+    bias_seed fixes the skew bias independently of the logits' seed (default:
+    the same seed).
+    """
     g = _gen(device, seed + 17000 + M)
     logits = torch.randn((M, E), generator=g, device=device, dtype=torch.float32)
     if skewed:
-        gb = _gen(device, seed + 29000)
+        gb = _gen(device, (seed if bias_seed is None else bias_seed) + 29000)
         bias = torch.randn((E,), generator=gb, device=device, dtype=torch.float32) * SKEW_STD
         logits = logits + bias
     vals, ids = torch.topk(logits, k=topk, dim=-1)

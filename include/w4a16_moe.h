@@ -144,6 +144,21 @@ int w4a16_moe_fused_experts_profiled(
     size_t workspace_bytes, void* stream, float stage_ms[4]);
 
 /*
+ * Launch a single stage of w4a16_moe_fused_experts on `stream`:
+ * 0 = expert sort, 1 = w13 + SiLU*up, 2 = w2 + routing weight, 3 = combine.
+ * Each stage reads what the previous stages left in `workspace`, so a full
+ * call with the same arguments and workspace must have run first.  Lets a
+ * benchmark time one kernel in isolation; no counterpart in the reference.
+ */
+int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
+                        const void* w13_packed, const void* w2_packed,
+                        const void* w13_scale, const void* w2_scale,
+                        const float* topk_weights, const int32_t* topk_ids,
+                        int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                        int64_t K, int64_t group_size, void* out, int64_t ld_out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Read the dropped-pair counter the last fused call left in `workspace`
  * (waits for `stream`).  No counterpart in the reference, which has no range
  * check on topk_ids.
