@@ -31,9 +31,12 @@ WS_HEADER = 2
 WS_OFFSETS = 3
 WS_INTER = 4
 WS_PARTIAL = 5
-WS_NFIELDS = 6
+WS_TILES = 6
+WS_GEMV_BLOCKS = 7
+WS_NFIELDS = 8
 
 FUSED_BLOCK_M = 16
+GEMV_MAX_TOKENS = 4
 
 EXPORTED_SYMBOLS = (
     "w4a16_moe_align_sizes",

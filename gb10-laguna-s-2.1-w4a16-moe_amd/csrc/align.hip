@@ -129,6 +129,40 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   }
   if (tid == 0) off[E] = total;
   __syncthreads();
+
+  // 3b. work lists of the fused call: MFMA tiles for heavy experts, the
+  // single block of every light expert for the GEMV path.
+  if (a.tiles) {
+    const int thr = a.gemv_max_tokens;
+    int nt_local = 0, ng_local = 0;
+    for (int i = 0; i < ipt; ++i) {
+      const int e = e0 + i;
+      if (e < E) {
+        const int c = tot[e];
+        nt_local += c > thr ? (c + kMfmaTileM - 1) / kMfmaTileM : 0;
+        ng_local += (c > 0 && c <= thr) ? 1 : 0;
+      }
+    }
+    int n_tiles = 0, n_gemv = 0;
+    int tbase = block_exclusive_scan(nt_local, wave_tot, &n_tiles);
+    int gbase = block_exclusive_scan(ng_local, wave_tot, &n_gemv);
+    for (int i = 0; i < ipt; ++i) {
+      const int e = e0 + i;
+      if (e >= E) continue;
+      const int c = tot[e];
+      if (c > thr) {
+        for (int s0 = 0; s0 < c; s0 += kMfmaTileM)
+          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(kMfmaTileM, c - s0), 0);
+      } else if (c > 0) {
+        a.gemv_blocks[gbase++] = off[e] / B;
+      }
+    }
+    if (tid == 0) {
+      a.n_tiles[0] = n_tiles;
+      a.n_gemv[0] = n_gemv;
+    }
+  }
+
   for (int i = tid; i < nw * E; i += nthr) cnt[i] += off[i % E];
   __syncthreads();
 

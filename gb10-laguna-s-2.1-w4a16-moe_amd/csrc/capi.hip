@@ -2,6 +2,8 @@
 // launch sequence align -> w13 -> w2 -> combine, all on the caller's stream.
 #include <limits.h>
 
+#include <algorithm>
+
 #include "../../include/w4a16_moe.h"
 #include "common.hpp"
 
@@ -34,7 +36,14 @@ struct Layout {
   size_t off[W4A16_WS_NFIELDS];
   size_t total;
   int64_t em, nb;
+  bool mfma;          // heavy experts run on the MFMA kernels
+  int64_t max_tiles;  // bound of the MFMA tile list
+  int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
 };
+
+// An expert with more than this many (token, slot) pairs runs on MFMA tiles;
+// the others stay on the GEMV kernels.  Must stay below the sort block (16).
+constexpr int kGemvMaxTokens = W4A16_GEMV_MAX_TOKENS;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -53,6 +62,13 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   st = align_sizes(M, topk, E, W4A16_FUSED_BLOCK_M, &L->em, &L->nb);
   if (st) return st;
   const size_t n_tok = (size_t)(M * topk);
+  // MFMA tiles need whole 256-row weight tiles on both GEMMs; tiny batches
+  // cannot give an expert enough pairs to pay for the extra launches.
+  L->mfma = M > kGemvMaxTokens && (2 * N) % kMfmaTileN == 0 && K % kMfmaTileN == 0;
+  const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (kGemvMaxTokens + 1));
+  L->max_tiles = L->mfma ? (int64_t)n_tok / kMfmaTileM + heavy : 0;
+  L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
+                        : std::min<int64_t>((int64_t)n_tok, L->nb);
   size_t cur = 0;
   auto put = [&](int field, size_t bytes) {
     L->off[field] = cur;
@@ -64,6 +80,8 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   put(W4A16_WS_OFFSETS, (size_t)(E + 1) * sizeof(int32_t));
   put(W4A16_WS_INTER, n_tok * (size_t)N * sizeof(uint16_t));
   put(W4A16_WS_PARTIAL, n_tok * (size_t)K * sizeof(float));
+  put(W4A16_WS_TILES, (size_t)std::max<int64_t>(L->max_tiles, 1) * 4 * sizeof(int32_t));
+  put(W4A16_WS_GEMV_BLOCKS, (size_t)std::max<int64_t>(L->max_gemv, 1) * sizeof(int32_t));
   L->total = cur;
   return W4A16_OK;
 }
@@ -121,7 +139,10 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   (void)hipGetLastError();
   if (ev && hipEventRecord(ev[0], stream) != hipSuccess) return W4A16_ERR_HIP;
 
-  AlignLaunch al;
+  int4* tiles = reinterpret_cast<int4*>(ws + L.off[W4A16_WS_TILES]);
+  int32_t* gemv_blocks = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_GEMV_BLOCKS]);
+
+  AlignLaunch al{};
   al.ids = a.ids;
   al.n_tok = n_tok;
   al.num_experts = (int32_t)a.E;
@@ -133,10 +154,18 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   al.num_post = header;
   al.offsets = offsets;
   al.dropped = header + 1;
+  if (L.mfma) {
+    al.tiles = tiles;
+    al.n_tiles = header + 2;
+    al.gemv_blocks = gemv_blocks;
+    al.n_gemv = header + 3;
+    al.gemv_max_tokens = kGemvMaxTokens;
+  }
   if (want(0) && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
 
-  GemvLaunch g;
+  GemvLaunch g{};
+  g.block_list = L.mfma ? gemv_blocks : nullptr;
   g.sorted = sorted;
   g.expert_ids = eids;
   g.header = header;
@@ -144,7 +173,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.topk = (int32_t)a.topk;
   g.block = W4A16_FUSED_BLOCK_M;
   g.group = (int32_t)a.group;
-  g.max_blocks = (int32_t)(L.nb < n_tok ? L.nb : n_tok);
+  g.max_blocks = (int32_t)L.max_gemv;
   g.num_experts = (int32_t)a.E;
 
   g.act = static_cast<const uint16_t*>(a.hidden);
@@ -155,7 +184,27 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.out = inter;
   g.n_out = (int32_t)a.N;
   g.kdim = (int32_t)a.K;
+  MfmaLaunch m{};
+  m.sorted = sorted;
+  m.tiles = tiles;
+  m.header = header;
+  m.n_tok = n_tok;
+  m.topk = (int32_t)a.topk;
+  m.group = (int32_t)a.group;
+  m.max_tiles = (int32_t)L.max_tiles;
+
   if (want(1) && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (L.mfma && want(1)) {
+    m.act = g.act;
+    m.ld_act = g.ld_act;
+    m.w = g.w;
+    m.s = g.s;
+    m.topk_w = nullptr;
+    m.out = inter;
+    m.n_out = (int32_t)a.N;
+    m.kdim = (int32_t)a.K;
+    if (launch_w13_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
+  }
   if (ev && hipEventRecord(ev[2], stream) != hipSuccess) return W4A16_ERR_HIP;
 
   g.act = inter;
@@ -167,9 +216,20 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.n_out = (int32_t)a.K;
   g.kdim = (int32_t)a.N;
   if (want(2) && launch_w2_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (L.mfma && want(2)) {
+    m.act = inter;
+    m.ld_act = a.N;
+    m.w = g.w;
+    m.s = g.s;
+    m.topk_w = a.topk_w;
+    m.out = partial;
+    m.n_out = (int32_t)a.K;
+    m.kdim = (int32_t)a.N;
+    if (launch_w2_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
+  }
   if (ev && hipEventRecord(ev[3], stream) != hipSuccess) return W4A16_ERR_HIP;
 
-  CombineLaunch c;
+  CombineLaunch c{};
   c.partial = partial;
   c.ids = a.ids;
   c.out = static_cast<uint16_t*>(a.out);
@@ -225,7 +285,7 @@ int w4a16_moe_align_block_size(const int32_t* topk_ids, int64_t M, int64_t topk,
   if ((M > 0 && !topk_ids) || (em > 0 && !sorted_token_ids) || (nb > 0 && !expert_ids) ||
       !num_tokens_post_padded)
     return W4A16_ERR_NULL_POINTER;
-  AlignLaunch al;
+  AlignLaunch al{};
   al.ids = topk_ids;
   al.n_tok = (int32_t)(M * topk);
   al.num_experts = (int32_t)num_experts;

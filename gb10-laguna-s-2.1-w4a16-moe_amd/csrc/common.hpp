@@ -62,6 +62,10 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 // ---- host launchers (defined next to their kernels) ----------------------
 namespace w4a16 {
 
+// MFMA tile: token slots x weight rows of one workgroup.
+constexpr int kMfmaTileM = 128;
+constexpr int kMfmaTileN = 256;
+
 struct AlignLaunch {
   const int32_t* ids;
   int32_t n_tok;
@@ -74,6 +78,15 @@ struct AlignLaunch {
   int32_t* num_post;
   int32_t* offsets;  // may be null, [E+1]
   int32_t* dropped;  // may be null, [1]
+  // Work lists of the fused call (all null for the plain sort).  Experts
+  // with more than gemv_max_tokens pairs get MFMA tiles of up to
+  // kMfmaTileM slots; the others keep their single sorted block on the GEMV
+  // path.  Requires gemv_max_tokens < block.
+  int4* tiles;           // [max tiles] (expert, first slot, count, 0)
+  int32_t* n_tiles;      // [1]
+  int32_t* gemv_blocks;  // [max blocks] block indices, ascending
+  int32_t* n_gemv;       // [1]
+  int32_t gemv_max_tokens;
 };
 hipError_t launch_align(const AlignLaunch& a, hipStream_t stream);
 
@@ -95,9 +108,31 @@ struct GemvLaunch {
   int32_t group;
   int32_t max_blocks;      // upper bound of active blocks
   int32_t num_experts;
+  const int32_t* block_list;  // null: work item b is block b; else blocks
+                              // block_list[0 .. header[3])
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);
+
+struct MfmaLaunch {
+  const uint16_t* act;     // bf16 activation rows (x for w13, inter for w2)
+  int64_t ld_act;
+  const uint32_t* w;       // packed weights [E, rows_total, kdim/8]
+  const uint16_t* s;       // bf16 scales   [E, rows_total, kdim/G]
+  const int32_t* sorted;
+  const int4* tiles;       // (expert, first slot, count, 0)
+  const int32_t* header;   // [2] = number of tiles
+  const float* topk_w;     // w2 only
+  void* out;               // w13: bf16 inter [n_tok, n_out]; w2: fp32 [n_tok, n_out]
+  int32_t n_tok;
+  int32_t topk;
+  int32_t n_out;           // N for w13 (2N weight rows), K for w2
+  int32_t kdim;
+  int32_t group;
+  int32_t max_tiles;
+};
+hipError_t launch_w13_mfma(const MfmaLaunch& a, hipStream_t stream);
+hipError_t launch_w2_mfma(const MfmaLaunch& a, hipStream_t stream);
 
 struct CombineLaunch {
   const float* partial;    // [M*topk, K]

@@ -103,8 +103,13 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
 
   const int rows_per_wave = 8 * RPL;
   const int chunks = a.n_out / rows_per_wave;
-  const int blk = blockIdx.x / chunks;
-  const int chunk = blockIdx.x - blk * chunks;
+  const int item = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - item * chunks;
+  int blk = item;
+  if (a.block_list) {
+    if (item >= a.header[3]) return;
+    blk = a.block_list[item];
+  }
   if (blk * a.block >= a.header[0]) return;
   const int e = a.expert_ids[blk];
   if (e < 0) return;

@@ -54,14 +54,22 @@ extern "C" {
 #define W4A16_WS_SORTED_IDS   0  /* int32 [EM]            sorted token-slot ids   */
 #define W4A16_WS_EXPERT_IDS   1  /* int32 [EM/16]         expert of each block    */
 #define W4A16_WS_HEADER       2  /* int32 [64]: [0] num_tokens_post_padded,
-                                    [1] dropped pairs, [2..] reserved            */
+                                    [1] dropped pairs, [2] MFMA tiles,
+                                    [3] GEMV blocks, [4..] reserved              */
 #define W4A16_WS_OFFSETS      3  /* int32 [E+1]           padded expert offsets   */
 #define W4A16_WS_INTER        4  /* bf16  [M*topk, N]     SiLU(gate)*up           */
 #define W4A16_WS_PARTIAL      5  /* fp32  [M*topk, K]     weighted w2 products    */
-#define W4A16_WS_NFIELDS      6
+#define W4A16_WS_TILES        6  /* int32 [tiles][4]      MFMA work list          */
+#define W4A16_WS_GEMV_BLOCKS  7  /* int32 [blocks]        GEMV work list          */
+#define W4A16_WS_NFIELDS      8
 
 /* Token-block size the fused call uses for its internal expert sort. */
 #define W4A16_FUSED_BLOCK_M 16
+
+/* Experts with more (token, slot) pairs than this run on the MFMA kernels
+ * when M > this value and 2N and K are multiples of 256; the others run on
+ * the GEMV kernels. */
+#define W4A16_GEMV_MAX_TOKENS 4
 
 /*
  * Sizes of moe_align_block_size's outputs.

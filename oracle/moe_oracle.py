@@ -295,7 +295,7 @@ def _as_u8_tensor(w) -> torch.Tensor:
 def moe_reference(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
                   topk_weights: torch.Tensor, topk_ids: torch.Tensor, group: int = 32,
                   *, exact_weights: bool = False, round_inter: bool = False,
-                  out_dtype=torch.bfloat16) -> torch.Tensor:
+                  bf16_weight_experts=(), out_dtype=torch.bfloat16) -> torch.Tensor:
     """PyTorch CPU dequant reference for one MoE layer.
 
     Restates run_reference (bench/bench_moe.py:277-303): for every expert with
@@ -305,6 +305,8 @@ def moe_reference(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
     The dequantization runs inside (from the unchanged packed tensors).
 
     exact_weights: use (code-8)*scale without the bf16 rounding of the dequant.
+    bf16_weight_experts: experts that keep the bf16 rounding even when
+    exact_weights is set (a per-expert mix of both rounding points).
     round_inter: round SiLU(gate)*up to bf16 like the reference kernel does
     (kernels/w4a16_moe.py:489).
     """
@@ -326,8 +328,9 @@ def moe_reference(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
         if not bool(mask.any()):
             continue
         token_idx, slot_idx = mask.nonzero(as_tuple=True)
-        W13 = _dequant_torch(w13b[e], s13[e], group, exact_weights)  # [2N, K]
-        W2 = _dequant_torch(w2b[e], s2[e], group, exact_weights)  # [K, N]
+        exact = exact_weights and e not in bf16_weight_experts
+        W13 = _dequant_torch(w13b[e], s13[e], group, exact)  # [2N, K]
+        W2 = _dequant_torch(w2b[e], s2[e], group, exact)  # [K, N]
         y = F.linear(h[token_idx], W13)
         a = F.silu(y[:, :N]) * y[:, N:]
         if round_inter:

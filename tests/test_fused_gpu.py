@@ -40,7 +40,24 @@ def _ulp_bf16(v: torch.Tensor) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(a)) - 7)
 
 
-def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True):
+def mfma_experts(pkg, ti, E, N, K):
+    """Experts the fused call runs on the MFMA kernels (bf16-rounded weights).
+
+    Restates the dispatch rule of the C library: when M > GEMV_MAX_TOKENS and
+    2N and K are multiples of 256, experts with more than GEMV_MAX_TOKENS
+    routed pairs go to MFMA tiles.
+    """
+    thr = pkg._lib.GEMV_MAX_TOKENS
+    M = ti.shape[0]
+    if not (M > thr and (2 * N) % 256 == 0 and K % 256 == 0):
+        return set()
+    ids = ti.reshape(-1).cpu()
+    ids = ids[(ids >= 0) & (ids < E)]
+    counts = torch.bincount(ids.to(torch.int64), minlength=E)
+    return {int(e) for e in torch.nonzero(counts > thr).reshape(-1)}
+
+
+def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True, bf16_experts=()):
     out32 = out.float().cpu()
     ref = orc.moe_reference(x, w13, w2, s13, s2, tw, ti, group, out_dtype=None)
     rl2 = orc.rel_l2(out32, ref)
@@ -52,7 +69,8 @@ def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True):
     assert mab <= 2e-2 * scale, msg
     if tight:
         t = orc.moe_reference(x, w13, w2, s13, s2, tw, ti, group, exact_weights=True,
-                              round_inter=True, out_dtype=None)
+                              round_inter=True, bf16_weight_experts=bf16_experts,
+                              out_dtype=None)
         trl2 = orc.rel_l2(out32, t)
         # Error sources vs the tight oracle: the final bf16 rounding (<= half an
         # ulp of the element) plus fp32 summation-order noise and rare one-ulp
@@ -71,6 +89,9 @@ def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True):
 
 SMALL = [
     # E, topk, K, N, group, M
+    (4, 2, 512, 256, 32, 300),    # MFMA: two 128-slot tiles per expert
+    (8, 4, 1024, 384, 64, 150),   # MFMA with group 64, N a multiple of 128 only
+    (6, 3, 256, 128, 128, 97),    # MFMA with group 128
     (8, 2, 256, 256, 32, 1),
     (8, 2, 256, 256, 32, 3),
     (16, 4, 512, 256, 32, 5),
@@ -92,7 +113,9 @@ def test_fused_small(pkg, orc, synth, dev, E, topk, K, N, group, M):
     out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group)
     torch.cuda.synchronize()
     assert out.shape == (M, K) and out.dtype == torch.bfloat16
-    _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag)
+    heavy = mfma_experts(pkg, ti, E, N, K)
+    print(f"{tag}: {len(heavy)} experts on the MFMA path", flush=True)
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, bf16_experts=heavy)
 
 
 def test_intermediate_matches_oracle(pkg, orc, synth, dev):
@@ -140,6 +163,24 @@ def test_internal_sort_matches_oracle(pkg, orc, synth, dev):
     assert np.array_equal(got_s, want[0])
     assert np.array_equal(got_e, want[1])
     assert hdr[0] == want[2][0] and hdr[1] == 0
+    # work lists: MFMA tiles of <= 128 slots for experts with more than
+    # GEMV_MAX_TOKENS pairs, the single block of every other routed expert
+    hdr = ws[off[2]: off[2] + 16].view(torch.int32).cpu().numpy()
+    thr = pkg._lib.GEMV_MAX_TOKENS
+    counts = np.bincount(ti.cpu().numpy().reshape(-1), minlength=shape.E)
+    offs = want[3]
+    tiles, gemv = [], []
+    for e in range(shape.E):
+        c = int(counts[e])
+        if c > thr:
+            tiles += [(e, int(offs[e]) + s0, min(128, c - s0)) for s0 in range(0, c, 128)]
+        elif c > 0:
+            gemv.append(int(offs[e]) // 16)
+    assert hdr[2] == len(tiles) and hdr[3] == len(gemv)
+    got_t = ws[off[6]: off[6] + 16 * len(tiles)].view(torch.int32).cpu().numpy()
+    assert [tuple(r[:3]) for r in got_t.reshape(-1, 4)] == tiles
+    got_g = ws[off[7]: off[7] + 4 * len(gemv)].view(torch.int32).cpu().numpy()
+    assert got_g.tolist() == gemv
 
 
 def test_deterministic(pkg, synth, dev):
@@ -163,7 +204,8 @@ def test_out_of_range_ids_dropped(pkg, orc, synth, dev):
     out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
     torch.cuda.synchronize()
     assert pkg.dropped_pairs(x, ti, w13, w2, 32) == 2
-    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "out-of-range ids")
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "out-of-range ids",
+           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
 
 
 def test_duplicate_ids_in_a_row(pkg, orc, synth, dev):
@@ -174,7 +216,8 @@ def test_duplicate_ids_in_a_row(pkg, orc, synth, dev):
                        [2, 2, 2, 3]], dtype=torch.int32, device=dev)
     out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
     torch.cuda.synchronize()
-    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "duplicate ids")
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "duplicate ids",
+           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
 
 
 def test_dtypes_and_strides(pkg, orc, synth, dev):
@@ -205,9 +248,9 @@ def test_zero_tokens(pkg, synth, dev):
     assert out.shape == (0, shape.K)
 
 
-def test_graph_capture_replay(pkg, synth, dev):
-    shape = synth.LayerShape(E=32, topk=4, K=512, N=256, group=32)
-    M = 4
+@pytest.mark.parametrize("M", [4, 40])
+def test_graph_capture_replay(pkg, synth, dev, M):
+    shape = synth.LayerShape(E=8, topk=4, K=512, N=256, group=32)
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=8)
     eager = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)  # creates workspace
     torch.cuda.synchronize()
@@ -253,7 +296,8 @@ def test_full_size_decode_configs(pkg, orc, synth, dev, full_layer, cfg_index):
     out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
     torch.cuda.synchronize()
     _check(orc, out, x.cpu(), c13, c2, cs13, cs2, tw.cpu(), ti.cpu(), 32,
-           f"config {cfg_index}", tight=cfg.M <= 16)
+           f"config {cfg_index}", tight=cfg.M <= 16,
+           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
 
 
 @pytest.mark.parametrize("cfg_index", [3, 4])
