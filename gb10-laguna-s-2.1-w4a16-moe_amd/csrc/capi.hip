@@ -62,9 +62,10 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   st = align_sizes(M, topk, E, W4A16_FUSED_BLOCK_M, &L->em, &L->nb);
   if (st) return st;
   const size_t n_tok = (size_t)(M * topk);
-  // MFMA tiles need whole 256-row weight tiles on both GEMMs; tiny batches
-  // cannot give an expert enough pairs to pay for the extra launches.
-  L->mfma = M > kGemvMaxTokens && (2 * N) % kMfmaTileN == 0 && K % kMfmaTileN == 0;
+  // MFMA tiles need whole 256-row weight tiles and whole 256-element weight
+  // slabs on both GEMMs; tiny batches cannot give an expert enough pairs to
+  // pay for the extra launches.
+  L->mfma = M > kGemvMaxTokens && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
   const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (kGemvMaxTokens + 1));
   L->max_tiles = L->mfma ? (int64_t)n_tok / kMfmaTileM + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)

@@ -110,6 +110,8 @@ struct GemvLaunch {
   int32_t num_experts;
   const int32_t* block_list;  // null: work item b is block b; else blocks
                               // block_list[0 .. header[3])
+  uint32_t nib_mask;          // set by the launcher (see gemv.hip)
+  uint32_t nib_magic;
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);

@@ -12,31 +12,33 @@
 // wave read 8 lines.  Each lane walks groups gi = 8*it + (lane % 8).
 //
 // Dequantisation never forms (code-8)*scale per weight.  A packed word w holds
-// codes n0..n7 for k = 8j..8j+7 (nibble i at bits 4i).  Four AND-OR ops make
-// four bf16 pairs whose values are the codes plus a constant:
-//   (w      & 0x000F000F) | 0x43004300 -> (128+n0, 128+n4)
-//   (w >> 1 & 0x00780078) | 0x41804180 -> ( 16+n1,  16+n5)
-//   (w >> 8 & 0x000F000F) | 0x43004300 -> (128+n2, 128+n6)
-//   (w >> 9 & 0x00780078) | 0x41804180 -> ( 16+n3,  16+n7)
-// (0x4300 is bf16 128 with an integer-spaced mantissa; 0x4180 is bf16 16,
-// whose mantissa step at bit 3 is 1.)  v_dot2_f32_bf16 against the matching
-// activation pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7) accumulates
-//   P = sum_k (code_k + c_k) x_k,  c_k = 128 (k even) or 16 (k odd)
-// and the group's true partial sum is P - C with
-//   C = 136 * sum_{k even} x_k + 24 * sum_{k odd} x_k,
-// because the weight is code - 8.  C depends on the activation row only and
-// is computed once when the row is staged.  The scale is applied once per
-// group: y += s * (P - C).  Products of bf16 activations with small integers
-// are exact in fp32, so the only rounding is fp32 accumulation.
+// codes n0..n7 for k = 8j..8j+7 (nibble i at bits 4i).  One AND-OR per pair
+// (after a shift) makes bf16 pairs of value 128 + code:
+//   (w       & 0x000F000F) | 0x43004300 -> (128+n0, 128+n4)
+//   (w >>  4 & 0x000F000F) | 0x43004300 -> (128+n1, 128+n5)
+//   (w >>  8 & 0x000F000F) | 0x43004300 -> (128+n2, 128+n6)
+//   (w >> 12 & 0x000F000F) | 0x43004300 -> (128+n3, 128+n7)
+// (0x4300 is bf16 128, whose mantissa step is 1.)  v_dot2_f32_bf16 against
+// the matching activation pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7) accumulates
+//   P = sum_k (code_k + 128) x_k
+// and the group's true partial sum is P - C with C = 136 * sum_k x_k, because
+// the weight is code - 8.  C depends on the activation row only and is
+// computed once when the row is staged.  The scale is applied once per group:
+// y += s * (P - C).  Products of bf16 activations with small integers are
+// exact in fp32, so the only rounding is fp32 accumulation.
+//
+// The mask and the magic constant arrive as kernel arguments and the magic is
+// copied to a vector register once: as opaque registers (one scalar, one
+// vector) they let the compiler fuse each pair into one v_and_or_b32 -- with
+// immediate constants it emits a separate AND and OR.
+// Weight and scale addresses are 32-bit offsets from per-expert bases held in
+// scalar registers.
 #include "common.hpp"
 
 namespace w4a16 {
 namespace {
 
-constexpr uint32_t kMaskA = 0x000F000Fu;
-constexpr uint32_t kMaskB = 0x00780078u;
-constexpr uint32_t kMagicA = 0x43004300u;  // bf16 (128, 128)
-constexpr uint32_t kMagicB = 0x41804180u;  // bf16 (16, 16)
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // LDS index of activation octet u (8 bf16 values) in a staged row: one pad
 // octet after every 32-element group spreads the 8 lanes of a row over
@@ -54,35 +56,36 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 // Sum over one packed word (8 codes) against its permuted activation octet.
-__device__ __forceinline__ float word_dot(uint32_t w, const uint4& x, float acc) {
-  acc = dot2((w & kMaskA) | kMagicA, x.x, acc);
-  acc = dot2(((w >> 1) & kMaskB) | kMagicB, x.y, acc);
-  acc = dot2(((w >> 8) & kMaskA) | kMagicA, x.z, acc);
-  acc = dot2(((w >> 9) & kMaskB) | kMagicB, x.w, acc);
+__device__ __forceinline__ float word_dot(uint32_t w, const u32x4_t& x, float acc,
+                                          uint32_t mask, uint32_t magic) {
+  acc = dot2((w & mask) | magic, x[0], acc);
+  acc = dot2(((w >> 4) & mask) | magic, x[1], acc);
+  acc = dot2(((w >> 8) & mask) | magic, x[2], acc);
+  acc = dot2(((w >> 12) & mask) | magic, x[3], acc);
   return acc;
 }
 
 // Stage one bf16 activation row of kdim values into LDS, permuted into the
 // pair order word_dot expects, plus the per-group offset correction C.
 __device__ __forceinline__ void stage_row(const uint16_t* __restrict__ src,
-                                          int kdim, uint4* xp, float* xc) {
+                                          int kdim, u32x4_t* xp, float* xc) {
   const int lane = __lane_id();
   const int n_oct = kdim >> 3;
-  const uint4* s4 = reinterpret_cast<const uint4*>(src);
+  const u32x4_t* s4 = reinterpret_cast<const u32x4_t*>(src);
   for (int u0 = 0; u0 < n_oct; u0 += 64) {
     const int u = u0 + lane;
-    uint4 d = make_uint4(0u, 0u, 0u, 0u);
+    u32x4_t d = {0u, 0u, 0u, 0u};
     if (u < n_oct) d = s4[u];
-    const float x0 = bf16_to_f32(d.x & 0xFFFFu), x1 = bf16_to_f32(d.x >> 16);
-    const float x2 = bf16_to_f32(d.y & 0xFFFFu), x3 = bf16_to_f32(d.y >> 16);
-    const float x4 = bf16_to_f32(d.z & 0xFFFFu), x5 = bf16_to_f32(d.z >> 16);
-    const float x6 = bf16_to_f32(d.w & 0xFFFFu), x7 = bf16_to_f32(d.w >> 16);
-    float c = 136.0f * ((x0 + x2) + (x4 + x6)) + 24.0f * ((x1 + x3) + (x5 + x7));
-    uint4 p;
-    p.x = (d.x & 0xFFFFu) | (d.z << 16);          // (x0, x4)
-    p.y = (d.x >> 16) | (d.z & 0xFFFF0000u);      // (x1, x5)
-    p.z = (d.y & 0xFFFFu) | (d.w << 16);          // (x2, x6)
-    p.w = (d.y >> 16) | (d.w & 0xFFFF0000u);      // (x3, x7)
+    const float x0 = bf16_to_f32(d[0] & 0xFFFFu), x1 = bf16_to_f32(d[0] >> 16);
+    const float x2 = bf16_to_f32(d[1] & 0xFFFFu), x3 = bf16_to_f32(d[1] >> 16);
+    const float x4 = bf16_to_f32(d[2] & 0xFFFFu), x5 = bf16_to_f32(d[2] >> 16);
+    const float x6 = bf16_to_f32(d[3] & 0xFFFFu), x7 = bf16_to_f32(d[3] >> 16);
+    float c = 136.0f * (((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)));
+    u32x4_t p;
+    p[0] = (d[0] & 0xFFFFu) | (d[2] << 16);      // (x0, x4)
+    p[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);  // (x1, x5)
+    p[2] = (d[1] & 0xFFFFu) | (d[3] << 16);      // (x2, x6)
+    p[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);  // (x3, x7)
     if (u < n_oct) xp[lds_octet(u)] = p;
     c = quad_sum(c);  // the 4 octets of a group sit in one lane quad
     if (u < n_oct && (lane & 3) == 0) xc[u >> 2] = c;
@@ -99,7 +102,7 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 template <int MODE, int RPL, int PF, int TC>
 __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
   constexpr int NR = MODE == 0 ? 2 * RPL : RPL;  // weight rows per lane
-  extern __shared__ uint4 lds[];
+  extern __shared__ u32x4_t lds[];
 
   const int rows_per_wave = 8 * RPL;
   const int chunks = a.n_out / rows_per_wave;
@@ -127,9 +130,17 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
   const int gshift = a.group == 32 ? 0 : (a.group == 64 ? 1 : 2);
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
   const int n_base = chunk * rows_per_wave + r;
+  // The magic constant lives in a VGPR: v_and_or_b32 may read only one scalar
+  // operand, so with both constants in SGPRs the compiler would split it.
+  const uint32_t mask = a.nib_mask;
+  uint32_t magic;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.nib_magic));
 
-  const uint4* wrow[NR];
-  const uint16_t* srow[NR];
+  // Uniform per-expert bases, per-lane 32-bit row offsets (one expert's rows
+  // span well under 4 GB).
+  const char* wexp = reinterpret_cast<const char*>(a.w) + (int64_t)e * rows_total * G * 16;
+  const char* sexp = reinterpret_cast<const char*>(a.s) + (int64_t)e * rows_total * gpr * 2;
+  uint32_t woff[NR], soff[NR];
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     int row;
@@ -137,13 +148,12 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
       row = (j < RPL) ? n_base + 8 * j : a.n_out + n_base + 8 * (j - RPL);
     else
       row = n_base + 8 * j;
-    const int64_t grow = (int64_t)e * rows_total + row;
-    wrow[j] = reinterpret_cast<const uint4*>(a.w) + grow * G;
-    srow[j] = a.s + grow * gpr;
+    woff[j] = (uint32_t)row * (uint32_t)G * 16u;
+    soff[j] = (uint32_t)row * (uint32_t)gpr * 2u;
   }
 
   const int row_oct = staged_row_octets(kdim);
-  uint4* xp = lds;
+  u32x4_t* xp = lds;
   float* xc = reinterpret_cast<float*>(lds + TC * row_oct);
   const int n_it = (G + 7) >> 3;
 
@@ -153,17 +163,17 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
     // Weight and raw bf16 scale registers of PF steps in flight.  Scales
     // stay as raw bits until use: converting right after the load would make
     // the compiler wait for it there and serialise the prefetch ring.
-    uint4 wb[PF][NR];
+    u32x4_t wb[PF][NR];
     uint32_t sb[PF][NR];
     // Loads are unconditional so the waitcnt pass sees the same number of
     // loads in flight on every path: steps past the row end re-read the last
     // step's lines (cache hits) and their results are never used.
-    auto load_step = [&](uint4 (&wq)[NR], uint32_t (&sq)[NR], int it) {
-      const int gi = min(min(it, n_it - 1) * 8 + sl, G - 1);
+    auto load_step = [&](u32x4_t (&wq)[NR], uint32_t (&sq)[NR], int it) {
+      const uint32_t gi = (uint32_t)min(min(it, n_it - 1) * 8 + sl, G - 1);
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        wq[j] = wrow[j][gi];
-        sq[j] = srow[j][gi >> gshift];
+        wq[j] = *reinterpret_cast<const u32x4_t*>(wexp + (woff[j] + gi * 16u));
+        sq[j] = *reinterpret_cast<const uint16_t*>(sexp + (soff[j] + (gi >> gshift) * 2u));
       }
     };
 #pragma unroll
@@ -195,15 +205,15 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
 #pragma unroll
           for (int t = 0; t < TC; ++t) {
             if (t < tc) {
-              const uint4* xg = xp + t * row_oct + lds_octet(gl * 4);
-              const uint4 x0 = xg[0], x1 = xg[1], x2 = xg[2], x3 = xg[3];
+              const u32x4_t* xg = xp + t * row_oct + lds_octet(gl * 4);
+              const u32x4_t x0 = xg[0], x1 = xg[1], x2 = xg[2], x3 = xg[3];
               const float c = xc[t * G + gl];
 #pragma unroll
               for (int j = 0; j < NR; ++j) {
-                float pj = word_dot(wb[p][j].x, x0, 0.0f);
-                pj = word_dot(wb[p][j].y, x1, pj);
-                pj = word_dot(wb[p][j].z, x2, pj);
-                pj = word_dot(wb[p][j].w, x3, pj);
+                float pj = word_dot(wb[p][j][0], x0, 0.0f, mask, magic);
+                pj = word_dot(wb[p][j][1], x1, pj, mask, magic);
+                pj = word_dot(wb[p][j][2], x2, pj, mask, magic);
+                pj = word_dot(wb[p][j][3], x3, pj, mask, magic);
                 const float sc = in ? bf16_to_f32(sb[p][j]) : 0.0f;
                 acc[j][t] = fmaf(sc, pj - c, acc[j][t]);
               }
@@ -250,12 +260,13 @@ constexpr size_t kMaxLds = 65536;
 
 size_t gemv_lds_bytes(int tc, int kdim) {
   const size_t row_oct = (size_t)(kdim >> 3) + (kdim >> 5);
-  return tc * (row_oct * sizeof(uint4) + (size_t)(kdim >> 5) * sizeof(float));
+  return tc * (row_oct * sizeof(u32x4_t) + (size_t)(kdim >> 5) * sizeof(float));
 }
 
 template <int MODE, int RPL, int PF, int TC>
 hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
   const int rows_per_wave = 8 * RPL;
+  if (a.n_out % rows_per_wave != 0) return hipErrorInvalidValue;
   const int chunks = a.n_out / rows_per_wave;
   const size_t lds = gemv_lds_bytes(TC, a.kdim);
   if (lds > kMaxLds) return hipErrorInvalidValue;
@@ -266,7 +277,6 @@ hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Activation rows staged per pass: fewer rows keep more waves resident.
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts
 // get one or two pairs; beyond that stage four rows per pass.
 int pick_tc(const GemvLaunch& a, int num_experts) {
@@ -282,19 +292,42 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
 
 }  // namespace
 
-hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream) {
+// Launch shapes: output rows per lane (RPL) and prefetch depth (PF) of the
+// two GEMVs.  Overridable at build time for tuning sweeps.
+#ifndef W4A16_W13_RPL
+#define W4A16_W13_RPL 2
+#endif
+#ifndef W4A16_W13_PF
+#define W4A16_W13_PF 3
+#endif
+#ifndef W4A16_W2_RPL
+#define W4A16_W2_RPL 4
+#endif
+#ifndef W4A16_W2_PF
+#define W4A16_W2_PF 2
+#endif
+
+hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
+  GemvLaunch a = a_in;
+  a.nib_mask = 0x000F000Fu;
+  a.nib_magic = 0x43004300u;  // bf16 (128, 128)
+  constexpr int R = W4A16_W13_RPL, P = W4A16_W13_PF;
   switch (pick_tc(a, a.num_experts)) {
-    case 1: return launch_gemv_t<0, 2, 3, 1>(a, stream);
-    case 2: return launch_gemv_t<0, 2, 3, 2>(a, stream);
-    default: return launch_gemv_t<0, 2, 3, 4>(a, stream);
+    case 1: return launch_gemv_t<0, R, P, 1>(a, stream);
+    case 2: return launch_gemv_t<0, R, P, 2>(a, stream);
+    default: return launch_gemv_t<0, R, P, 4>(a, stream);
   }
 }
 
-hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream) {
+hipError_t launch_w2_gemv(const GemvLaunch& a_in, hipStream_t stream) {
+  GemvLaunch a = a_in;
+  a.nib_mask = 0x000F000Fu;
+  a.nib_magic = 0x43004300u;
+  constexpr int R = W4A16_W2_RPL, P = W4A16_W2_PF;
   switch (pick_tc(a, a.num_experts)) {
-    case 1: return launch_gemv_t<1, 4, 2, 1>(a, stream);
-    case 2: return launch_gemv_t<1, 4, 2, 2>(a, stream);
-    default: return launch_gemv_t<1, 4, 2, 4>(a, stream);
+    case 1: return launch_gemv_t<1, R, P, 1>(a, stream);
+    case 2: return launch_gemv_t<1, R, P, 2>(a, stream);
+    default: return launch_gemv_t<1, R, P, 4>(a, stream);
   }
 }
 

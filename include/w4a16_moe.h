@@ -67,7 +67,7 @@ extern "C" {
 #define W4A16_FUSED_BLOCK_M 16
 
 /* Experts with more (token, slot) pairs than this run on the MFMA kernels
- * when M > this value and 2N and K are multiples of 256; the others run on
+ * when M > this value and N and K are multiples of 256; the others run on
  * the GEMV kernels. */
 #define W4A16_GEMV_MAX_TOKENS 4
 

@@ -44,12 +44,12 @@ def mfma_experts(pkg, ti, E, N, K):
     """Experts the fused call runs on the MFMA kernels (bf16-rounded weights).
 
     Restates the dispatch rule of the C library: when M > GEMV_MAX_TOKENS and
-    2N and K are multiples of 256, experts with more than GEMV_MAX_TOKENS
+    N and K are multiples of 256, experts with more than GEMV_MAX_TOKENS
     routed pairs go to MFMA tiles.
     """
     thr = pkg._lib.GEMV_MAX_TOKENS
     M = ti.shape[0]
-    if not (M > thr and (2 * N) % 256 == 0 and K % 256 == 0):
+    if not (M > thr and N % 256 == 0 and K % 256 == 0):
         return set()
     ids = ti.reshape(-1).cpu()
     ids = ids[(ids >= 0) & (ids < E)]
@@ -90,8 +90,9 @@ def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True, bf16_e
 SMALL = [
     # E, topk, K, N, group, M
     (4, 2, 512, 256, 32, 300),    # MFMA: two 128-slot tiles per expert
-    (8, 4, 1024, 384, 64, 150),   # MFMA with group 64, N a multiple of 128 only
-    (6, 3, 256, 128, 128, 97),    # MFMA with group 128
+    (8, 4, 1024, 512, 64, 150),   # MFMA with group 64
+    (6, 3, 256, 256, 128, 97),    # MFMA with group 128
+    (8, 4, 1024, 384, 64, 150),   # N not a multiple of 256: GEMV only, many tokens
     (8, 2, 256, 256, 32, 1),
     (8, 2, 256, 256, 32, 3),
     (16, 4, 512, 256, 32, 5),
