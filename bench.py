@@ -56,6 +56,9 @@ MALL_BYTES = 256 * 2**20       # Infinity Cache
 # 226.3 GB/s on NVIDIA GB10 (results/showdown2.json:1104; README.md:62-70).
 REFERENCE_GBS_M16 = 226.3
 STAGES = ("align", "w13", "w2", "combine")
+CALIB_BYTES = 512 * 2**20       # plain device copy used to scale the PMC byte counters
+# Kernel-name fragments of the dominant kernels in rocprofv3 counter files.
+KERNEL_KEYS = {"w13": "gemv_kernel<0,", "w2": "gemv_kernel<1,"}
 
 
 def log(*a):
@@ -250,6 +253,65 @@ def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
     }
 
 
+def calibration_copy(dev):
+    """One plain device-to-device copy of CALIB_BYTES, for PMC calibration."""
+    import torch
+
+    a = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+
+
+def traffic_from_pmc(pmc_dirs, kernel_key):
+    """HBM bytes per launch of a kernel from rocprofv3 --pmc CSV output.
+
+    pmc_dirs: directories holding *_counter_collection.csv of a FETCH_SIZE run
+    and of a WRITE_SIZE run of a command that also ran calibration_copy().
+    Each counter is scaled by CALIB_BYTES / (its reading on the copy kernel).
+    Returns (bytes, detail) or (None, reason).
+    """
+    import csv
+    import glob
+
+    sums = {}
+    for d in pmc_dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            rows = list(csv.DictReader(open(path)))
+            for name in ("FETCH_SIZE", "WRITE_SIZE"):
+                sel = [r for r in rows if r["Counter_Name"] == name]
+                if not sel:
+                    continue
+                copies = [float(r["Counter_Value"]) for r in sel
+                          if "copyBuffer" in r["Kernel_Name"]]
+                mine = [float(r["Counter_Value"]) for r in sel if kernel_key in r["Kernel_Name"]]
+                if not copies or not mine:
+                    continue
+                calib_kib = max(copies)
+                factor = (CALIB_BYTES / 1024.0) / calib_kib
+                sums[name] = (sum(mine) / len(mine) * 1024.0 * factor, factor, len(mine))
+    if "FETCH_SIZE" not in sums or "WRITE_SIZE" not in sums:
+        return None, "no FETCH_SIZE/WRITE_SIZE readings for the kernel and the copy"
+    total = sums["FETCH_SIZE"][0] + sums["WRITE_SIZE"][0]
+    detail = {k: {"bytes": int(v[0]), "scale": round(v[1], 4), "dispatches": v[2]}
+              for k, v in sums.items()}
+    return int(total), detail
+
+
+def traffic_from_profile(kernel, config_index):
+    """The HBM bytes per launch recorded in profiles/ for this kernel/config."""
+    import re
+
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            m = re.match(r"\s*traffic\[(\w+), config (\d+)\]:\s*(\d+)\s*bytes", line)
+            if m and m.group(1) == kernel and int(m.group(2)) == config_index:
+                return int(m.group(3)), str(path.relative_to(ROOT))
+    return None, None
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -260,6 +322,11 @@ def main(argv=None) -> int:
     p.add_argument("--no-sweep", action="store_true", help="skip the other configs")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--stage-replays", type=int, default=8)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help=f"run one {CALIB_BYTES >> 20} MiB device copy first (PMC calibration)")
+    p.add_argument("--pmc-dir", action="append", default=[],
+                   help="rocprofv3 --pmc output dirs (FETCH_SIZE and WRITE_SIZE runs of this "
+                        "command with --calibrate-copy) to derive roofline.traffic from")
     args = p.parse_args(argv)
 
     if args.gpus != 1:
@@ -279,6 +346,8 @@ def main(argv=None) -> int:
         return 2
     dev = torch.device("cuda:0")
     shape = synth.LayerShape()
+    if args.calibrate_copy:
+        calibration_copy(dev)
     log(f"device {torch.cuda.get_device_name(0)}; generating weights "
         f"({shape.E * shape.bytes_per_expert / 1e9:.2f} GB)")
     weights = synth.make_weights(shape, dev, seed=0)
@@ -297,6 +366,13 @@ def main(argv=None) -> int:
     dominant = "w13" if stages["w13"] >= stages["w2"] else "w2"
     dom_bytes = sum(getattr(wl, f"{dominant}_bytes")) / len(wl.sets)
     achieved = dom_bytes / (stages[dominant] * 1e-3) / 1e9
+    traffic, traffic_src = None, None
+    if args.pmc_dir:
+        traffic, detail = traffic_from_pmc(args.pmc_dir, KERNEL_KEYS[dominant])
+        traffic_src = {"pmc": detail}
+    else:
+        traffic, path = traffic_from_profile(dominant, head_cfg.index)
+        traffic_src = path
     roofline = {
         "bound": "hbm",
         "kernel": f"{dominant} dequant-GEMV (gemv_kernel)",
@@ -304,7 +380,8 @@ def main(argv=None) -> int:
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": traffic_src,
         "avg_launch_us": round(stages[dominant] * 1e3, 3),
         "algorithmic_bytes_per_launch": int(dom_bytes),
     }
