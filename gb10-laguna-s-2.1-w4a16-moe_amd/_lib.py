@@ -37,6 +37,7 @@ WS_NFIELDS = 8
 
 FUSED_BLOCK_M = 16
 GEMV_MAX_TOKENS = 4
+GEMV_ONLY_MAX_M = 16
 
 EXPORTED_SYMBOLS = (
     "w4a16_moe_align_sizes",

@@ -44,6 +44,7 @@ struct Layout {
 // An expert with more than this many (token, slot) pairs runs on MFMA tiles;
 // the others stay on the GEMV kernels.  Must stay below the sort block (16).
 constexpr int kGemvMaxTokens = W4A16_GEMV_MAX_TOKENS;
+constexpr int kGemvOnlyMaxM = W4A16_GEMV_ONLY_MAX_M;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -63,9 +64,9 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   if (st) return st;
   const size_t n_tok = (size_t)(M * topk);
   // MFMA tiles need whole 256-row weight tiles and whole 256-element weight
-  // slabs on both GEMMs; tiny batches cannot give an expert enough pairs to
+  // slabs on both GEMMs; small batches cannot give an expert enough pairs to
   // pay for the extra launches.
-  L->mfma = M > kGemvMaxTokens && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
+  L->mfma = M > kGemvOnlyMaxM && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
   const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (kGemvMaxTokens + 1));
   L->max_tiles = L->mfma ? (int64_t)n_tok / kMfmaTileM + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)

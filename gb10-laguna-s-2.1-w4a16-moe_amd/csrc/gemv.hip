@@ -5,12 +5,14 @@
 // repacked layout and feed tl.dot.  This file reads the unchanged
 // pack-quantized rows instead (one row = one output channel, K contiguous).
 //
-// Work item = one wave: one 16-slot expert block x a slab of output rows.
+// Work item = one workgroup of WAVES waves: one 16-slot expert block x
+// WAVES slabs of output rows, one slab per wave.  The block's activation rows
+// are staged into LDS once by the whole workgroup and shared by its waves.
 // Lane layout: 8 lanes per weight row, each lane owns whole 32-element groups
 // (one 16-byte dwordx4 = 4 packed words = 32 int4 codes), so the 8 lanes of a
 // row read one contiguous 128-byte line per step and the 8 row groups of a
 // wave read 8 lines.  Each lane walks groups gi = 8*it + (lane % 8).
-//
+
 // Dequantisation never forms (code-8)*scale per weight.  A packed word w holds
 // codes n0..n7 for k = 8j..8j+7 (nibble i at bits 4i).  One AND-OR per pair
 // (after a shift) makes bf16 pairs of value 128 + code:
@@ -23,7 +25,8 @@
 //   P = sum_k (code_k + 128) x_k
 // and the group's true partial sum is P - C with C = 136 * sum_k x_k, because
 // the weight is code - 8.  C depends on the activation row only and is
-// computed once when the row is staged.  The scale is applied once per group:
+// computed once when the row is staged; the dot2 chain of a group starts from
+// -C, so it ends at P - C.  The scale is applied once per group:
 // y += s * (P - C).  Products of bf16 activations with small integers are
 // exact in fp32, so the only rounding is fp32 accumulation.
 //
@@ -33,6 +36,8 @@
 // immediate constants it emits a separate AND and OR.
 // Weight and scale addresses are 32-bit offsets from per-expert bases held in
 // scalar registers.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace w4a16 {
@@ -42,11 +47,12 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // LDS index of activation octet u (8 bf16 values) in a staged row: one pad
 // octet after every 32-element group spreads the 8 lanes of a row over
-// distinct banks.
+// distinct banks.  A staged row of G groups is followed by one zero group
+// (with C = 0): steps past the row end read it and add exactly nothing.
 __device__ __forceinline__ int lds_octet(int u) { return u + (u >> 2); }
 
-__device__ __forceinline__ int staged_row_octets(int kdim) {
-  return (kdim >> 3) + (kdim >> 5);
+__host__ __device__ __forceinline__ int staged_row_octets(int kdim) {
+  return 5 * ((kdim >> 5) + 1);
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -66,48 +72,64 @@ __device__ __forceinline__ float word_dot(uint32_t w, const u32x4_t& x, float ac
 }
 
 // Stage one bf16 activation row of kdim values into LDS, permuted into the
-// pair order word_dot expects, plus the per-group offset correction C.
-__device__ __forceinline__ void stage_row(const uint16_t* __restrict__ src,
-                                          int kdim, u32x4_t* xp, float* xc) {
-  const int lane = __lane_id();
+// pair order word_dot expects, plus the per-group offset correction C.  All
+// NT threads of the workgroup take part.
+template <int NT>
+__device__ __forceinline__ void stage_row(const uint16_t* __restrict__ src, int kdim,
+                                          u32x4_t* xp, float* xc) {
+  const int tid = threadIdx.x;
   const int n_oct = kdim >> 3;
   const u32x4_t* s4 = reinterpret_cast<const u32x4_t*>(src);
-  for (int u0 = 0; u0 < n_oct; u0 += 64) {
-    const int u = u0 + lane;
+  // octets n_oct .. n_oct+3 form the zero group
+  for (int u0 = 0; u0 < n_oct + 4; u0 += NT) {
+    const int u = u0 + tid;
     u32x4_t d = {0u, 0u, 0u, 0u};
     if (u < n_oct) d = s4[u];
     const float x0 = bf16_to_f32(d[0] & 0xFFFFu), x1 = bf16_to_f32(d[0] >> 16);
     const float x2 = bf16_to_f32(d[1] & 0xFFFFu), x3 = bf16_to_f32(d[1] >> 16);
     const float x4 = bf16_to_f32(d[2] & 0xFFFFu), x5 = bf16_to_f32(d[2] >> 16);
     const float x6 = bf16_to_f32(d[3] & 0xFFFFu), x7 = bf16_to_f32(d[3] >> 16);
-    float c = 136.0f * (((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)));
+    float c = -136.0f * (((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)));
     u32x4_t p;
     p[0] = (d[0] & 0xFFFFu) | (d[2] << 16);      // (x0, x4)
     p[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);  // (x1, x5)
     p[2] = (d[1] & 0xFFFFu) | (d[3] << 16);      // (x2, x6)
     p[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);  // (x3, x7)
-    if (u < n_oct) xp[lds_octet(u)] = p;
+    if (u < n_oct + 4) xp[lds_octet(u)] = p;
     c = quad_sum(c);  // the 4 octets of a group sit in one lane quad
-    if (u < n_oct && (lane & 3) == 0) xc[u >> 2] = c;
+    if (u < n_oct + 4 && (tid & 3) == 0) xc[u >> 2] = c;  // -C
   }
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
+#ifndef GEMV_MIN_WAVES
+#define GEMV_MIN_WAVES 1
+#endif
+
 // MODE 0: w13 rows (gate n, up N+n), epilogue SiLU(gate)*up -> bf16 inter.
 // MODE 1: w2 rows, epilogue * topk weight -> fp32 partial.
-// RPL: output rows per lane (w13: gate+up pairs, so 2*RPL weight rows).
-// PF:  weight loads kept in flight, in groups-steps.
-// TC:  activation rows staged per pass.
-template <int MODE, int RPL, int PF, int TC>
-__global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
+// RPL:   output rows per lane (w13: gate+up pairs, so 2*RPL weight rows).
+// PF:    weight loads kept in flight, in group steps.
+// TC:    activation rows staged per pass.
+// WAVES: waves per workgroup (row slabs sharing one staged block).
+// NIT:   group steps per row (ceil(kdim / 256)) when fixed at compile time,
+//        0 for any other length.
+template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(GEMV_MIN_WAVES)))
+void gemv_kernel(const GemvLaunch a) {
   constexpr int NR = MODE == 0 ? 2 * RPL : RPL;  // weight rows per lane
+  constexpr int NT = 64 * WAVES;
   extern __shared__ u32x4_t lds[];
 
   const int rows_per_wave = 8 * RPL;
-  const int chunks = a.n_out / rows_per_wave;
-  const int item = blockIdx.x / chunks;
-  const int chunk = blockIdx.x - item * chunks;
+  const int chunks = a.n_out / rows_per_wave;           // row slabs per block
+  const int slabs = (chunks + WAVES - 1) / WAVES;       // workgroups per block
+  const int item = blockIdx.x / slabs;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int chunk_raw = (blockIdx.x - item * slabs) * WAVES + wid;
+  const bool has_rows = chunk_raw < chunks;             // wave-uniform
+  const int chunk = has_rows ? chunk_raw : chunks - 1;  // idle waves re-read a slab
   int blk = item;
   if (a.block_list) {
     if (item >= a.header[3]) return;
@@ -153,128 +175,214 @@ __global__ __launch_bounds__(64) void gemv_kernel(const GemvLaunch a) {
   }
 
   const int row_oct = staged_row_octets(kdim);
+  const int xc_pitch = G + 1;
   u32x4_t* xp = lds;
   float* xc = reinterpret_cast<float*>(lds + TC * row_oct);
   const int n_it = (G + 7) >> 3;
 
-  for (int t0 = 0; t0 < T; t0 += TC) {
-    const int tc = min(TC, T - t0);
-
+  // The whole item for NTOK (compile-time) tokens per pass.  Every variant
+  // owns its prefetch ring: sharing one ring between variants lets the
+  // register allocator reuse a ring register for activations, after which
+  // each step waits for every load in flight.  With NIT > 0 (the step count
+  // known at compile time) the step loop is fully unrolled and nothing is in
+  // flight across a loop edge, so every wait the compiler places is exact.
+  auto body = [&](auto ntok_c) {
+    constexpr int NTOK = decltype(ntok_c)::value;
     // Weight and raw bf16 scale registers of PF steps in flight.  Scales
     // stay as raw bits until use: converting right after the load would make
     // the compiler wait for it there and serialise the prefetch ring.
     u32x4_t wb[PF][NR];
     uint32_t sb[PF][NR];
-    // Loads are unconditional so the waitcnt pass sees the same number of
-    // loads in flight on every path: steps past the row end re-read the last
-    // step's lines (cache hits) and their results are never used.
     auto load_step = [&](u32x4_t (&wq)[NR], uint32_t (&sq)[NR], int it) {
-      const uint32_t gi = (uint32_t)min(min(it, n_it - 1) * 8 + sl, G - 1);
+      // An opaque step index keeps the address math at this point: with a
+      // constant index the compiler computes every step's addresses up front
+      // and holds them in registers.
+      asm volatile("" : "+s"(it));
+      const uint32_t gi = (uint32_t)min(it * 8 + sl, G - 1);
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         wq[j] = *reinterpret_cast<const u32x4_t*>(wexp + (woff[j] + gi * 16u));
         sq[j] = *reinterpret_cast<const uint16_t*>(sexp + (soff[j] + (gi >> gshift) * 2u));
       }
     };
+    // One group step: 8 lanes per row, lane sl on group 8*it + sl; steps past
+    // the row end meet the zero activation group and add nothing.
+    auto compute_step = [&](const u32x4_t (&wq)[NR], const uint32_t (&sq)[NR], int it,
+                            float (&acc)[NR][NTOK]) {
+      const int gi = it * 8 + sl;
+      const int gl = gi < G ? gi : G;
+      float pj[NR][NTOK];
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load_step(wb[p], sb[p], p);
-
-    // Stage this pass's activation rows.
-    __syncthreads();
-    for (int t = 0; t < tc; ++t) {
-      const int f = __shfl(f_lane, t0 + t, 64);
-      const int64_t arow = MODE == 0 ? f / a.topk : f;
-      stage_row(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * G);
-    }
-    __syncthreads();
-
-    float acc[NR][TC];
+      for (int t = 0; t < NTOK; ++t) {
+        const float c = xc[t * xc_pitch + gl];  // -C
 #pragma unroll
-    for (int j = 0; j < NR; ++j)
+        for (int j = 0; j < NR; ++j) pj[j][t] = c;
+      }
 #pragma unroll
-      for (int t = 0; t < TC; ++t) acc[j][t] = 0.0f;
-
-    for (int it0 = 0; it0 < n_it; it0 += PF) {
+      for (int w = 0; w < 4; ++w) {
+        u32x4_t x[NTOK];
 #pragma unroll
-      for (int p = 0; p < PF; ++p) {
-        const int it = it0 + p;
-        if (it < n_it) {  // wave-uniform; no loads inside
-          const int gi = it * 8 + sl;
-          const bool in = gi < G;
-          const int gl = in ? gi : G - 1;
+        for (int t = 0; t < NTOK; ++t) x[t] = xp[t * row_oct + lds_octet(gl * 4 + w)];
 #pragma unroll
-          for (int t = 0; t < TC; ++t) {
-            if (t < tc) {
-              const u32x4_t* xg = xp + t * row_oct + lds_octet(gl * 4);
-              const u32x4_t x0 = xg[0], x1 = xg[1], x2 = xg[2], x3 = xg[3];
-              const float c = xc[t * G + gl];
+        for (int j = 0; j < NR; ++j) {
+          const uint32_t wv = wq[j][w];
+          const uint32_t d0 = (wv & mask) | magic;
+          const uint32_t d1 = ((wv >> 4) & mask) | magic;
+          const uint32_t d2 = ((wv >> 8) & mask) | magic;
+          const uint32_t d3 = ((wv >> 12) & mask) | magic;
 #pragma unroll
-              for (int j = 0; j < NR; ++j) {
-                float pj = word_dot(wb[p][j][0], x0, 0.0f, mask, magic);
-                pj = word_dot(wb[p][j][1], x1, pj, mask, magic);
-                pj = word_dot(wb[p][j][2], x2, pj, mask, magic);
-                pj = word_dot(wb[p][j][3], x3, pj, mask, magic);
-                const float sc = in ? bf16_to_f32(sb[p][j]) : 0.0f;
-                acc[j][t] = fmaf(sc, pj - c, acc[j][t]);
-              }
-            }
+          for (int t = 0; t < NTOK; ++t) {
+            float q = dot2(d0, x[t][0], pj[j][t]);
+            q = dot2(d1, x[t][1], q);
+            q = dot2(d2, x[t][2], q);
+            pj[j][t] = dot2(d3, x[t][3], q);
           }
         }
-        load_step(wb[p], sb[p], it + PF);
+        // One word's activation reads at a time (NTOK * 4 registers); the
+        // other waves of the SIMD cover the LDS latency.
+        if (NTOK > 1) __builtin_amdgcn_sched_barrier(0);
       }
-    }
-
-    // Reduce each row over its 8 lanes; lane sl then owns token t0+sl.
-#pragma unroll
-    for (int j = 0; j < NR; ++j)
-#pragma unroll
-      for (int t = 0; t < TC; ++t) acc[j][t] = oct_sum(acc[j][t]);
-
-    const int f_mine = __shfl(f_lane, min(t0 + sl, 63), 64);
-    if (sl < tc) {
-      float v[NR];
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        v[j] = acc[j][0];
+        const float sc = bf16_to_f32(sq[j]);
 #pragma unroll
-        for (int t = 1; t < TC; ++t)
-          if (sl == t) v[j] = acc[j][t];
+        for (int t = 0; t < NTOK; ++t) {
+          acc[j][t] = fmaf(sc, pj[j][t], acc[j][t]);
+          // Pin the step's math here: left alone, the compiler sinks it
+          // towards the final reduction and keeps every loaded step alive.
+          asm volatile("" : "+v"(acc[j][t]));
+        }
       }
-      if (MODE == 0) {
-        uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
+    };
+
+    for (int t0 = 0; t0 < T; t0 += NTOK) {
+      const int tc = min(NTOK, T - t0);  // tokens past tc compute unused values
+      // Opaque row offsets per pass: otherwise every load address of the pass
+      // is loop-invariant, gets hoisted out of the pass loop and stays live
+      // in registers for the whole kernel.
 #pragma unroll
-        for (int q = 0; q < RPL; ++q)
-          out[n_base + 8 * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
+      for (int j = 0; j < NR; ++j) asm volatile("" : "+v"(woff[j]), "+v"(soff[j]));
+
+#pragma unroll
+      for (int p = 0; p < PF; ++p)
+        if (NIT == 0 || p < NIT) load_step(wb[p], sb[p], min(p, n_it - 1));
+
+      // Stage this pass's activation rows (the whole workgroup).
+      __syncthreads();
+      for (int t = 0; t < tc; ++t) {
+        const int f = __shfl(f_lane, t0 + t, 64);
+        const int64_t arow = MODE == 0 ? f / a.topk : f;
+        stage_row<NT>(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * xc_pitch);
+      }
+      __syncthreads();
+
+      float acc[NR][NTOK];
+#pragma unroll
+      for (int j = 0; j < NR; ++j)
+#pragma unroll
+        for (int t = 0; t < NTOK; ++t) acc[j][t] = 0.0f;
+
+      if constexpr (NIT > 0) {
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          compute_step(wb[it % PF], sb[it % PF], it, acc);
+          if (it + PF < NIT) load_step(wb[it % PF], sb[it % PF], it + PF);
+          // Straight-line code: keep each step's loads behind the earlier
+          // steps' math, or the scheduler hoists them all and the registers
+          // they hold cost occupancy.
+          __builtin_amdgcn_sched_barrier(0);
+        }
       } else {
-        const float wt = a.topk_w[f_mine];
-        float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
+        // Step count known only at run time: loads stay unconditional (steps
+        // past the row end re-read the last group's line, a cache hit) so
+        // the same number of loads is in flight on every path.
+        for (int it0 = 0; it0 < n_it; it0 += PF) {
 #pragma unroll
-        for (int q = 0; q < RPL; ++q) out[n_base + 8 * q] = v[q] * wt;
+          for (int p = 0; p < PF; ++p) {
+            const int it = it0 + p;
+            if (it < n_it) compute_step(wb[p], sb[p], it, acc);  // wave-uniform
+            load_step(wb[p], sb[p], min(it + PF, n_it - 1));
+          }
+        }
+      }
+
+      // Reduce each row over its 8 lanes; lane sl then owns token t0+sl.
+#pragma unroll
+      for (int j = 0; j < NR; ++j)
+#pragma unroll
+        for (int t = 0; t < NTOK; ++t) acc[j][t] = oct_sum(acc[j][t]);
+
+      const int f_mine = __shfl(f_lane, min(t0 + sl, 63), 64);
+      if (has_rows && sl < tc) {
+        float v[NR];
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+          v[j] = acc[j][0];
+#pragma unroll
+          for (int t = 1; t < NTOK; ++t)
+            if (sl == t) v[j] = acc[j][t];
+        }
+        if (MODE == 0) {
+          uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
+#pragma unroll
+          for (int q = 0; q < RPL; ++q)
+            out[n_base + 8 * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
+        } else {
+          const float wt = a.topk_w[f_mine];
+          float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
+#pragma unroll
+          for (int q = 0; q < RPL; ++q) out[n_base + 8 * q] = v[q] * wt;
+        }
       }
     }
-  }
+  };
+
+  // One variant per block: T >= TC runs passes of TC tokens.
+  const int tcap = min(T, TC);
+  if (TC >= 4 && tcap >= 4) body(std::integral_constant<int, (TC >= 4 ? 4 : 1)>{});
+  else if (TC >= 3 && tcap == 3) body(std::integral_constant<int, (TC >= 3 ? 3 : 1)>{});
+  else if (TC >= 2 && tcap == 2) body(std::integral_constant<int, (TC >= 2 ? 2 : 1)>{});
+  else body(std::integral_constant<int, 1>{});
 }
 
 // The staged rows must fit the 64 KB of LDS a workgroup may use.
 constexpr size_t kMaxLds = 65536;
+#ifndef W4A16_GEMV_WAVES
+#define W4A16_GEMV_WAVES 4
+#endif
+constexpr int kGemvWaves = W4A16_GEMV_WAVES;
 
 size_t gemv_lds_bytes(int tc, int kdim) {
-  const size_t row_oct = (size_t)(kdim >> 3) + (kdim >> 5);
-  return tc * (row_oct * sizeof(u32x4_t) + (size_t)(kdim >> 5) * sizeof(float));
+  const size_t row_oct = (size_t)staged_row_octets(kdim);
+  return tc * (row_oct * sizeof(u32x4_t) + (size_t)((kdim >> 5) + 1) * sizeof(float));
 }
 
-template <int MODE, int RPL, int PF, int TC>
-hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
+template <int MODE, int RPL, int PF, int TC, int NIT>
+hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
+  constexpr int W = kGemvWaves;
   const int rows_per_wave = 8 * RPL;
   if (a.n_out % rows_per_wave != 0) return hipErrorInvalidValue;
   const int chunks = a.n_out / rows_per_wave;
+  const int slabs = (chunks + W - 1) / W;
   const size_t lds = gemv_lds_bytes(TC, a.kdim);
   if (lds > kMaxLds) return hipErrorInvalidValue;
-  const int64_t grid = (int64_t)a.max_blocks * chunks;
+  const int64_t grid = (int64_t)a.max_blocks * slabs;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC>), dim3((unsigned)grid), dim3(64),
-                     lds, stream, a);
+  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT>), dim3((unsigned)grid),
+                     dim3(64 * W), lds, stream, a);
   return hipGetLastError();
+}
+
+// Fully unrolled step loops for the row lengths of the target layer
+// (K = 3072: 12 steps; N = 1024: 4 steps); any other length runs the loop.
+template <int MODE, int RPL, int PF, int TC>
+hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
+  const int n_it = ((a.kdim >> 5) + 7) >> 3;
+  switch (n_it) {
+    case 4: return launch_gemv_n<MODE, RPL, PF, TC, 4>(a, stream);
+    case 12: return launch_gemv_n<MODE, RPL, PF, TC, 12>(a, stream);
+    default: return launch_gemv_n<MODE, RPL, PF, TC, 0>(a, stream);
+  }
 }
 
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts
@@ -293,18 +401,18 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
 }  // namespace
 
 // Launch shapes: output rows per lane (RPL) and prefetch depth (PF) of the
-// two GEMVs.  Overridable at build time for tuning sweeps.
+// two GEMVs, waves per workgroup.  Overridable at build time for tuning sweeps.
 #ifndef W4A16_W13_RPL
-#define W4A16_W13_RPL 2
+#define W4A16_W13_RPL 1
 #endif
 #ifndef W4A16_W13_PF
-#define W4A16_W13_PF 3
+#define W4A16_W13_PF 4
 #endif
 #ifndef W4A16_W2_RPL
-#define W4A16_W2_RPL 4
+#define W4A16_W2_RPL 2
 #endif
 #ifndef W4A16_W2_PF
-#define W4A16_W2_PF 2
+#define W4A16_W2_PF 3
 #endif
 
 hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {

@@ -67,9 +67,14 @@ extern "C" {
 #define W4A16_FUSED_BLOCK_M 16
 
 /* Experts with more (token, slot) pairs than this run on the MFMA kernels
- * when M > this value and N and K are multiples of 256; the others run on
- * the GEMV kernels. */
+ * when M > W4A16_GEMV_ONLY_MAX_M and N and K are multiples of 256; the others
+ * run on the GEMV kernels. */
 #define W4A16_GEMV_MAX_TOKENS 4
+
+/* Calls with at most this many tokens run every expert on the GEMV kernels:
+ * no expert can then hold more than one 16-slot block, and the MFMA
+ * launches would only add their fixed cost. */
+#define W4A16_GEMV_ONLY_MAX_M 16
 
 /*
  * Sizes of moe_align_block_size's outputs.

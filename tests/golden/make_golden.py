@@ -18,7 +18,7 @@ code that shares nothing with ``oracle/``:
 * ``moe_*.npz`` -- whole-layer cases (bench/bench_moe.py:271-303): inputs and
   the float64 output from bf16-rounded dequantized weights, computed with
   float64 numpy matrix products.  ``moe_gemv`` routes at most 4 pairs to each
-  expert; ``moe_mfma`` routes more (the matrix-core path of the kernels).
+  expert; ``moe_mfma`` (M = 24 > 16) routes more (the matrix-core path).
 
 Usage:  python tests/golden/make_golden.py
 """
@@ -216,7 +216,7 @@ def main() -> None:
     (HERE / "align_cases.json").write_text(json.dumps(align_cases(), separators=(",", ":")))
     (HERE / "dequant_cases.json").write_text(json.dumps(dequant_cases(), indent=1))
     moe_case("moe_gemv", M=6, E=8, topk=4, K=256, N=64, group=32, seed=11, heavy=False)
-    moe_case("moe_mfma", M=12, E=2, topk=2, K=256, N=256, group=64, seed=12, heavy=True)
+    moe_case("moe_mfma", M=24, E=2, topk=2, K=256, N=256, group=64, seed=12, heavy=True)
 
 
 if __name__ == "__main__":

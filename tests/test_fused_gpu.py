@@ -43,13 +43,13 @@ def _ulp_bf16(v: torch.Tensor) -> torch.Tensor:
 def mfma_experts(pkg, ti, E, N, K):
     """Experts the fused call runs on the MFMA kernels (bf16-rounded weights).
 
-    Restates the dispatch rule of the C library: when M > GEMV_MAX_TOKENS and
+    Restates the dispatch rule of the C library: when M > GEMV_ONLY_MAX_M and
     N and K are multiples of 256, experts with more than GEMV_MAX_TOKENS
     routed pairs go to MFMA tiles.
     """
     thr = pkg._lib.GEMV_MAX_TOKENS
     M = ti.shape[0]
-    if not (M > thr and N % 256 == 0 and K % 256 == 0):
+    if not (M > pkg._lib.GEMV_ONLY_MAX_M and N % 256 == 0 and K % 256 == 0):
         return set()
     ids = ti.reshape(-1).cpu()
     ids = ids[(ids >= 0) & (ids < E)]
