@@ -102,10 +102,14 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(const MfmaLaunch a) {
 
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
   const int n_tiles_n = rows_total / kTN;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  // The grid is sized for the most tiles a routing can produce; the align
+  // kernel wrote the real count.  Workgroups past it leave at once, and the
+  // XCD remap runs over the real ones so that every XCD gets its share.
+  const int n_active = a.header[2] * n_tiles_n;
+  if ((int)blockIdx.x >= n_active) return;
+  const int bid = xcd_remap(blockIdx.x, n_active);
   const int tile = bid / n_tiles_n;
   const int nt = bid - tile * n_tiles_n;
-  if (tile >= a.header[2]) return;
   const int4 info = a.tiles[tile];
   const int e = info.x, start = info.y, count = info.z;
 
