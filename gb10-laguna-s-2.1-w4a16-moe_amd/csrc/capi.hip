@@ -1,5 +1,6 @@
 // C ABI of the W4A16 MoE library: argument checks, workspace layout and the
-// launch sequence align -> w13 -> w2 -> combine, all on the caller's stream.
+// launch sequence align -> w13 -> w2 -> combine, all on the caller's stream
+// (no align for small batches, whose GEMV kernels route themselves).
 #include <limits.h>
 
 #include <algorithm>
@@ -37,8 +38,10 @@ struct Layout {
   size_t total;
   int64_t em, nb;
   bool mfma;          // heavy experts run on the MFMA kernels
+  bool route;         // GEMV kernels route themselves; no align, no combine
   int64_t max_tiles;  // bound of the MFMA tile list
   int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
+  int64_t max_items;  // bound of the self-routed work items (experts)
 };
 
 // An expert with more than this many (token, slot) pairs runs on MFMA tiles;
@@ -71,6 +74,11 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   L->max_tiles = L->mfma ? (int64_t)n_tok / kMfmaTileM + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
                         : std::min<int64_t>((int64_t)n_tok, L->nb);
+  // Small batches: the GEMV kernels route themselves from topk_ids (work
+  // item = one routed expert), so the align kernel is not run.
+  L->route = !L->mfma && M >= 1 && M <= kGemvOnlyMaxM &&
+             gemv_route_fits((int)n_tok, (int)E, (int)K, (int)N);
+  L->max_items = L->route ? std::min<int64_t>(E, (int64_t)n_tok) : 0;
   size_t cur = 0;
   auto put = [&](int field, size_t bytes) {
     L->off[field] = cur;
@@ -163,7 +171,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
     al.n_gemv = header + 3;
     al.gemv_max_tokens = kGemvMaxTokens;
   }
-  if (want(0) && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(0) && !L.route && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
 
   GemvLaunch g{};
@@ -177,6 +185,11 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.group = (int32_t)a.group;
   g.max_blocks = (int32_t)L.max_gemv;
   g.num_experts = (int32_t)a.E;
+  if (L.route) {
+    g.ids = a.ids;
+    g.max_items = (int32_t)L.max_items;
+    g.dropped_out = header + 1;
+  }
 
   g.act = static_cast<const uint16_t*>(a.hidden);
   g.ld_act = a.ld_hidden;

@@ -57,6 +57,39 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// Exclusive scan of one int per thread over a workgroup of NT threads
+// (NT <= 1024); wave_tot is LDS scratch of 17 ints.  All threads must call.
+template <int NT>
+__device__ __forceinline__ int wg_exclusive_scan(int v, int* wave_tot, int* total) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wave_tot[wid] = x;
+  __syncthreads();
+  if (wid == 0) {
+    const int t = lane < NW ? wave_tot[lane] : 0;
+    int s = t;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(s, d, 64);
+      if (lane >= d) s += y;
+    }
+    if (lane < NW) wave_tot[lane] = s - t;
+    if (lane == NW - 1) wave_tot[16] = s;
+  }
+  __syncthreads();
+  *total = wave_tot[16];
+  const int excl = x - v + wave_tot[wid];
+  __syncthreads();
+  return excl;
+}
+
 }  // namespace w4a16
 
 // ---- host launchers (defined next to their kernels) ----------------------
@@ -112,9 +145,17 @@ struct GemvLaunch {
                               // block_list[0 .. header[3])
   uint32_t nib_mask;          // set by the launcher (see gemv.hip)
   uint32_t nib_magic;
+  // Self-routing (small batches, the align kernel is not run): when `ids`
+  // is set, work item i is the i-th expert with routed pairs, found by every
+  // workgroup from topk_ids itself.
+  const int32_t* ids;      // [n_tok] topk_ids
+  int32_t max_items;       // grid bound of the number of routed experts
+  int32_t* dropped_out;    // w13: [1] pairs with ids outside [0, E)
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);
+// Self-routing: whether the routing tables plus one staged row fit in LDS.
+bool gemv_route_fits(int n_tok, int num_experts, int K, int N);
 
 struct MfmaLaunch {
   const uint16_t* act;     // bf16 activation rows (x for w13, inter for w2)

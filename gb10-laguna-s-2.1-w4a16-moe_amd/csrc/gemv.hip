@@ -107,6 +107,92 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 #define GEMV_MIN_WAVES 1
 #endif
 
+// Self-routing tables in LDS after the staged rows (ints): ids, expert
+// flags, the item's flat indices, per-wave counts and scalars.
+__host__ __device__ __forceinline__ int route_ints(int n_tok, int num_experts) {
+  return 2 * n_tok + num_experts + 24;
+}
+
+// Work item `item` is the item-th expert (ascending) that has routed pairs;
+// its pairs in ascending flat index are the order moe_align_block_size gives
+// them (kernels/w4a16_moe.py:243-278).  Found from topk_ids directly: fills
+// r_ids[n_tok], r_slots[0..t_out) and r_misc[17] (pairs with ids outside
+// [0, E)).  e_out = -1 when item is past the last routed expert.  All NT
+// threads must call; every exit is workgroup-uniform.
+template <int NT>
+__device__ __forceinline__ void route_expert(const GemvLaunch& a, int item, int* r_ids,
+                                             int* r_flag, int* r_slots, int* r_misc,
+                                             int& e_out, int& t_out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  constexpr int NW = NT / 64;
+  const int n_tok = a.n_tok, E = a.num_experts;
+  const uint64_t below = lanemask_lt();
+  for (int i = tid; i < E; i += NT) r_flag[i] = 0;
+  if (tid == 0) {
+    r_misc[16] = -1;
+    r_misc[17] = 0;
+  }
+  __syncthreads();
+  int drop = 0;
+  for (int f = tid; f < n_tok; f += NT) {
+    const int e = a.ids[f];
+    r_ids[f] = e;
+    if (e >= 0 && e < E)
+      r_flag[e] = 1;
+    else
+      ++drop;
+  }
+  if (drop) atomicAdd(&r_misc[17], drop);
+  __syncthreads();
+
+  // The item-th used expert: ballot counts per wave, prefix over the waves.
+  int base = 0;
+  for (int e0 = 0; e0 < E; e0 += NT) {
+    const int e = e0 + tid;
+    const bool used = e < E && r_flag[e] != 0;
+    const uint64_t b = ballot(used);
+    if (lane == 0) r_misc[wid] = __popcll(b);
+    __syncthreads();
+    int wp = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int c = r_misc[w];
+      wp += w < wid ? c : 0;
+      tot += c;
+    }
+    if (used && base + wp + __popcll(b & below) == item) r_misc[16] = e;
+    base += tot;
+    __syncthreads();
+  }
+  const int e_sel = r_misc[16];
+  e_out = e_sel;
+  t_out = 0;
+  if (e_sel < 0) return;
+
+  // Its pairs, ascending flat index.
+  int cnt = 0;
+  for (int f0 = 0; f0 < n_tok; f0 += NT) {
+    const int f = f0 + tid;
+    const bool hit = f < n_tok && r_ids[f] == e_sel;
+    const uint64_t b = ballot(hit);
+    if (lane == 0) r_misc[wid] = __popcll(b);
+    __syncthreads();
+    int wp = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int c = r_misc[w];
+      wp += w < wid ? c : 0;
+      tot += c;
+    }
+    if (hit) r_slots[cnt + wp + __popcll(b & below)] = f;
+    cnt += tot;
+    __syncthreads();
+  }
+  t_out = cnt;
+}
+
 // MODE 0: w13 rows (gate n, up N+n), epilogue SiLU(gate)*up -> bf16 inter.
 // MODE 1: w2 rows, epilogue * topk weight -> fp32 partial.
 // RPL:   output rows per lane (w13: gate+up pairs, so 2*RPL weight rows).
@@ -115,7 +201,9 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // WAVES: waves per workgroup (row slabs sharing one staged block).
 // NIT:   group steps per row (ceil(kdim / 256)) when fixed at compile time,
 //        0 for any other length.
-template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT>
+// ROUTE: the workgroup routes itself from topk_ids (no align kernel); work
+//        item i is the i-th expert with routed pairs, all of its pairs.
+template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT, bool ROUTE>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(GEMV_MIN_WAVES)))
 void gemv_kernel(const GemvLaunch a) {
   constexpr int NR = MODE == 0 ? 2 * RPL : RPL;  // weight rows per lane
@@ -126,25 +214,53 @@ void gemv_kernel(const GemvLaunch a) {
   const int chunks = a.n_out / rows_per_wave;           // row slabs per block
   const int slabs = (chunks + WAVES - 1) / WAVES;       // workgroups per block
   const int item = blockIdx.x / slabs;
+  const int slab = blockIdx.x - item * slabs;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int chunk_raw = (blockIdx.x - item * slabs) * WAVES + wid;
+  const int chunk_raw = slab * WAVES + wid;
   const bool has_rows = chunk_raw < chunks;             // wave-uniform
   const int chunk = has_rows ? chunk_raw : chunks - 1;  // idle waves re-read a slab
-  int blk = item;
-  if (a.block_list) {
-    if (item >= a.header[3]) return;
-    blk = a.block_list[item];
-  }
-  if (blk * a.block >= a.header[0]) return;
-  const int e = a.expert_ids[blk];
-  if (e < 0) return;
-
+  const int tid = threadIdx.x;
   const int lane = __lane_id();
+  const int E = a.num_experts;
+
+  // LDS: staged activation rows | their -C values | routing tables
+  const int G0 = a.kdim >> 5;
+  const int row_oct = staged_row_octets(a.kdim);
+  const int xc_pitch = G0 + 1;
+  u32x4_t* xp = lds;
+  float* xc = reinterpret_cast<float*>(lds + TC * row_oct);
+  int* r_ids = reinterpret_cast<int*>(xc + TC * xc_pitch);
+  int* r_flag = r_ids + a.n_tok;
+  int* r_slots = r_flag + E;
+  int* r_misc = r_slots + a.n_tok;
+
+  int e, T, f_lane = 0;
+  if constexpr (ROUTE) {
+    route_expert<NT>(a, item, r_ids, r_flag, r_slots, r_misc, e, T);
+    if (MODE == 0 && blockIdx.x == 0 && tid == 0) a.dropped_out[0] = r_misc[17];
+    if (e < 0) return;
+  } else {
+    int blk = item;
+    if (a.block_list) {
+      if (item >= a.header[3]) return;
+      blk = a.block_list[item];
+    }
+    if (blk * a.block >= a.header[0]) return;
+    e = a.expert_ids[blk];
+    if (e < 0) return;
+    f_lane = lane < a.block ? a.sorted[blk * a.block + lane] : a.n_tok;
+    T = __popcll(ballot(f_lane < a.n_tok));  // valid slots are a prefix
+  }
+  // Flat index of the item's t-th pair (t < T).
+  auto slot_of = [&](int t) -> int {
+    if constexpr (ROUTE)
+      return r_slots[t];
+    else
+      return __shfl(f_lane, t, 64);
+  };
+
   const int r = lane >> 3;
   const int sl = lane & 7;
-
-  const int f_lane = lane < a.block ? a.sorted[blk * a.block + lane] : a.n_tok;
-  const int T = __popcll(ballot(f_lane < a.n_tok));  // valid slots are a prefix
 
   const int kdim = a.kdim;
   const int G = kdim >> 5;               // 32-element groups per row
@@ -174,10 +290,6 @@ void gemv_kernel(const GemvLaunch a) {
     soff[j] = (uint32_t)row * (uint32_t)gpr * 2u;
   }
 
-  const int row_oct = staged_row_octets(kdim);
-  const int xc_pitch = G + 1;
-  u32x4_t* xp = lds;
-  float* xc = reinterpret_cast<float*>(lds + TC * row_oct);
   const int n_it = (G + 7) >> 3;
 
   // The whole item for NTOK (compile-time) tokens per pass.  Every variant
@@ -270,7 +382,7 @@ void gemv_kernel(const GemvLaunch a) {
       // Stage this pass's activation rows (the whole workgroup).
       __syncthreads();
       for (int t = 0; t < tc; ++t) {
-        const int f = __shfl(f_lane, t0 + t, 64);
+        const int f = slot_of(t0 + t);
         const int64_t arow = MODE == 0 ? f / a.topk : f;
         stage_row<NT>(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * xc_pitch);
       }
@@ -312,7 +424,7 @@ void gemv_kernel(const GemvLaunch a) {
 #pragma unroll
         for (int t = 0; t < NTOK; ++t) acc[j][t] = oct_sum(acc[j][t]);
 
-      const int f_mine = __shfl(f_lane, min(t0 + sl, 63), 64);
+      const int f_mine = slot_of(min(t0 + sl, T - 1));
       if (has_rows && sl < tc) {
         float v[NR];
 #pragma unroll
@@ -357,32 +469,43 @@ size_t gemv_lds_bytes(int tc, int kdim) {
   return tc * (row_oct * sizeof(u32x4_t) + (size_t)((kdim >> 5) + 1) * sizeof(float));
 }
 
-template <int MODE, int RPL, int PF, int TC, int NIT>
+template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE>
 hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   constexpr int W = kGemvWaves;
   const int rows_per_wave = 8 * RPL;
   if (a.n_out % rows_per_wave != 0) return hipErrorInvalidValue;
   const int chunks = a.n_out / rows_per_wave;
   const int slabs = (chunks + W - 1) / W;
-  const size_t lds = gemv_lds_bytes(TC, a.kdim);
+  size_t lds = gemv_lds_bytes(TC, a.kdim);
+  if (ROUTE) lds += sizeof(int) * (size_t)route_ints(a.n_tok, a.num_experts);
   if (lds > kMaxLds) return hipErrorInvalidValue;
-  const int64_t grid = (int64_t)a.max_blocks * slabs;
+  const int64_t grid = (int64_t)(ROUTE ? a.max_items : a.max_blocks) * slabs;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT, ROUTE>), dim3((unsigned)grid),
                      dim3(64 * W), lds, stream, a);
   return hipGetLastError();
 }
 
 // Fully unrolled step loops for the row lengths of the target layer
 // (K = 3072: 12 steps; N = 1024: 4 steps); any other length runs the loop.
-template <int MODE, int RPL, int PF, int TC>
-hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
+template <int MODE, int RPL, int PF, int TC, bool ROUTE>
+hipError_t launch_gemv_r(const GemvLaunch& a, hipStream_t stream) {
   const int n_it = ((a.kdim >> 5) + 7) >> 3;
   switch (n_it) {
-    case 4: return launch_gemv_n<MODE, RPL, PF, TC, 4>(a, stream);
-    case 12: return launch_gemv_n<MODE, RPL, PF, TC, 12>(a, stream);
-    default: return launch_gemv_n<MODE, RPL, PF, TC, 0>(a, stream);
+    case 4: return launch_gemv_n<MODE, RPL, PF, TC, 4, ROUTE>(a, stream);
+    case 12: return launch_gemv_n<MODE, RPL, PF, TC, 12, ROUTE>(a, stream);
+    default: return launch_gemv_n<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
   }
+}
+
+template <int MODE, int RPL, int PF, int TC>
+hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
+  return a.ids ? launch_gemv_r<MODE, RPL, PF, TC, true>(a, stream)
+               : launch_gemv_r<MODE, RPL, PF, TC, false>(a, stream);
+}
+
+size_t route_bytes(const GemvLaunch& a) {
+  return a.ids ? sizeof(int) * (size_t)route_ints(a.n_tok, a.num_experts) : 0;
 }
 
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts
@@ -394,7 +517,7 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
     tc = 1;
   else if (a.n_tok <= num_experts)
     tc = 2;
-  while (tc > 1 && gemv_lds_bytes(tc, a.kdim) > kMaxLds) tc >>= 1;
+  while (tc > 1 && gemv_lds_bytes(tc, a.kdim) + route_bytes(a) > kMaxLds) tc >>= 1;
   return tc;
 }
 
@@ -425,6 +548,11 @@ hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
     case 2: return launch_gemv_t<0, R, P, 2>(a, stream);
     default: return launch_gemv_t<0, R, P, 4>(a, stream);
   }
+}
+
+bool gemv_route_fits(int n_tok, int num_experts, int K, int N) {
+  const size_t route = sizeof(int) * (size_t)route_ints(n_tok, num_experts);
+  return gemv_lds_bytes(1, K) + route <= kMaxLds && gemv_lds_bytes(1, N) + route <= kMaxLds;
 }
 
 hipError_t launch_w2_gemv(const GemvLaunch& a_in, hipStream_t stream) {

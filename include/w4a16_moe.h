@@ -62,6 +62,10 @@ extern "C" {
 #define W4A16_WS_TILES        6  /* int32 [tiles][4]      MFMA work list          */
 #define W4A16_WS_GEMV_BLOCKS  7  /* int32 [blocks]        GEMV work list          */
 #define W4A16_WS_NFIELDS      8
+/* Calls with M <= W4A16_GEMV_ONLY_MAX_M skip the align kernel: the GEMV
+ * kernels route themselves from topk_ids.  Those calls write only the
+ * header's dropped count [1], INTER and PARTIAL; the other fields keep
+ * whatever they held. */
 
 /* Token-block size the fused call uses for its internal expert sort. */
 #define W4A16_FUSED_BLOCK_M 16
