@@ -139,7 +139,7 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
       const int e = e0 + i;
       if (e < E) {
         const int c = tot[e];
-        nt_local += c > thr ? (c + kMfmaTileM - 1) / kMfmaTileM : 0;
+        nt_local += c > thr ? (c + a.tile_m - 1) / a.tile_m : 0;
         ng_local += (c > 0 && c <= thr) ? 1 : 0;
       }
     }
@@ -151,8 +151,8 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
       if (e >= E) continue;
       const int c = tot[e];
       if (c > thr) {
-        for (int s0 = 0; s0 < c; s0 += kMfmaTileM)
-          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(kMfmaTileM, c - s0), 0);
+        for (int s0 = 0; s0 < c; s0 += a.tile_m)
+          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(a.tile_m, c - s0), 0);
       } else if (c > 0) {
         a.gemv_blocks[gbase++] = off[e] / B;
       }

@@ -38,7 +38,8 @@ struct Layout {
   size_t total;
   int64_t em, nb;
   bool mfma;          // heavy experts run on the MFMA kernels
-  bool route;         // GEMV kernels route themselves; no align, no combine
+  bool route;         // GEMV kernels route themselves; no align kernel
+  int tile_m;         // MFMA tile height (slots)
   int64_t max_tiles;  // bound of the MFMA tile list
   int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
   int64_t max_items;  // bound of the self-routed work items (experts)
@@ -71,7 +72,10 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // pay for the extra launches.
   L->mfma = M > kGemvOnlyMaxM && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
   const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (kGemvMaxTokens + 1));
-  L->max_tiles = L->mfma ? (int64_t)n_tok / kMfmaTileM + heavy : 0;
+  // 256-slot tiles once an average expert holds more than 128 pairs: the
+  // whole expert then shares one dequantization of its weights.
+  L->tile_m = kMfmaTileM;
+  L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
                         : std::min<int64_t>((int64_t)n_tok, L->nb);
   // Small batches: the GEMV kernels route themselves from topk_ids (work
@@ -170,6 +174,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
     al.gemv_blocks = gemv_blocks;
     al.n_gemv = header + 3;
     al.gemv_max_tokens = kGemvMaxTokens;
+    al.tile_m = L.tile_m;
   }
   if (want(0) && !L.route && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
@@ -207,6 +212,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   m.topk = (int32_t)a.topk;
   m.group = (int32_t)a.group;
   m.max_tiles = (int32_t)L.max_tiles;
+  m.tile_m = L.tile_m;
 
   if (want(1) && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (L.mfma && want(1)) {
