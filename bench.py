@@ -22,6 +22,11 @@ Per-kernel durations come from replaying graphs of one stage at a time
 kernels run on; the dominant kernel's algorithmic bytes / duration is the
 roofline "achieved" figure.
 
+Each configuration row also carries "router": the device time of the router
+step in front of the layer (w4a16_moe_router_topk_softmax: fp32 logits
+[M, 256] -> top-10 ids and softmax weights, bench/bench_moe.py:225-230) and its
+logits+outputs bytes per second.
+
 The CPU baseline is the oracle's PyTorch dequant reference
 (oracle/moe_oracle.py, a restatement of bench/bench_moe.py:277-303) timed on
 the host on a bounded sample of the same workload.
@@ -189,6 +194,39 @@ class Workload:
             result[name] = start.elapsed_time(end) / (replays * len(self.sets))
         del wss, outs
         return result
+
+
+def time_router(wl, replays):
+    """Average device time of the router step (logits -> top-k ids and weights)
+    at this configuration's M, graph-replayed over as many logits sets."""
+    import torch
+
+    shape, M = wl.shape, wl.cfg.M
+    sets = []
+    for i in range(len(wl.sets)):
+        g = torch.Generator(device=wl.dev).manual_seed(17000 + M + i)
+        sets.append(torch.randn((M, shape.E), generator=g, device=wl.dev))
+    outs = [(torch.empty((M, shape.topk), device=wl.dev),
+             torch.empty((M, shape.topk), dtype=torch.int32, device=wl.dev)) for _ in sets]
+    for x, o in zip(sets, outs):
+        wl.pkg.router_topk_softmax(x, shape.topk, out=o)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for x, o in zip(sets, outs):
+            wl.pkg.router_topk_softmax(x, shape.topk, out=o)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / (replays * len(sets))
+    nbytes = M * shape.E * 4 + M * shape.topk * 8
+    return {"us": round(ms * 1e3, 3), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 2)}
 
 
 def summarize(wl, t, stages):
@@ -361,6 +399,7 @@ def main(argv=None) -> int:
     log(f"timed {t['steps']} steps in {t['elapsed_ms']:.3f} ms (wall {t['wall_s']:.3f} s)")
     stages = wl.time_stages(args.stage_replays)
     head = summarize(wl, t, stages)
+    head["router"] = time_router(wl, 20)
     log(f"headline: {json.dumps(head)}")
 
     dominant = "w13" if stages["w13"] >= stages["w2"] else "w2"
@@ -397,6 +436,7 @@ def main(argv=None) -> int:
             tt = w.time_calls(steps, min(8, len(w.sets)))
             st = w.time_stages(2)
             row = summarize(w, tt, st)
+            row["router"] = time_router(w, 20)
             log(f"config {cfg.index}: {json.dumps(row)}")
             sweep.append(row)
             del w

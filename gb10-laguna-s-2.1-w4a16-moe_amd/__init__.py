@@ -19,5 +19,7 @@ from .w4a16_moe import (  # noqa: F401
     repack_weights,
     workspace_tensor,
 )
+from .routing import router_topk_softmax  # noqa: F401
 
-__all__ = ["fused_experts_w4a16", "repack_weights", "moe_align_block_size", "is_repacked"]
+__all__ = ["fused_experts_w4a16", "repack_weights", "moe_align_block_size", "is_repacked",
+           "router_topk_softmax"]

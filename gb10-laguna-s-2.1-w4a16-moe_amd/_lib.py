@@ -24,6 +24,11 @@ W4A16_ERR_WORKSPACE_TOO_SMALL = 4
 W4A16_ERR_MISALIGNED = 5
 W4A16_ERR_INVALID_BLOCK = 6
 W4A16_ERR_HIP = 7
+W4A16_ERR_UNSUPPORTED_DTYPE = 8
+
+LOGITS_F32 = 0
+LOGITS_BF16 = 1
+ROUTER_MAX_TOPK = 64
 
 WS_SORTED_IDS = 0
 WS_EXPERT_IDS = 1
@@ -48,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "w4a16_moe_fused_experts_profiled",
     "w4a16_moe_run_stage",
     "w4a16_moe_dropped_pairs",
+    "w4a16_moe_router_topk_softmax",
     "w4a16_moe_strerror",
     "w4a16_moe_abi_version",
 )
@@ -89,6 +95,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.w4a16_moe_run_stage.argtypes = [ctypes.c_int] + fused
     lib.w4a16_moe_dropped_pairs.restype = ctypes.c_int
     lib.w4a16_moe_dropped_pairs.argtypes = [_vp, ctypes.POINTER(ctypes.c_int32), _vp]
+    lib.w4a16_moe_router_topk_softmax.restype = ctypes.c_int
+    lib.w4a16_moe_router_topk_softmax.argtypes = [
+        _vp, ctypes.c_int, _i64, _i64, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]
 
 
 def lib() -> ctypes.CDLL:

@@ -281,6 +281,7 @@ const char* w4a16_moe_strerror(int status) {
     case W4A16_ERR_MISALIGNED: return "pointer or row stride misaligned";
     case W4A16_ERR_INVALID_BLOCK: return "invalid block_size";
     case W4A16_ERR_HIP: return "HIP runtime error";
+    case W4A16_ERR_UNSUPPORTED_DTYPE: return "unsupported logits dtype";
     default: return "unknown status";
   }
 }
@@ -422,6 +423,38 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count, void* stream)
       hipSuccess)
     return W4A16_ERR_HIP;
   return hipStreamSynchronize(s) == hipSuccess ? W4A16_OK : W4A16_ERR_HIP;
+}
+
+int w4a16_moe_router_topk_softmax(const void* logits, int logits_dtype,
+                                  int64_t ld_logits, int64_t M, int64_t num_experts,
+                                  int64_t topk, int renormalize, float* topk_weights,
+                                  int32_t* topk_ids, void* stream) {
+  if (logits_dtype != W4A16_LOGITS_F32 && logits_dtype != W4A16_LOGITS_BF16)
+    return W4A16_ERR_UNSUPPORTED_DTYPE;
+  if (M < 0 || num_experts < 1 || num_experts > kMaxExperts) return W4A16_ERR_INVALID_SHAPE;
+  if (topk < 1 || topk > W4A16_ROUTER_MAX_TOPK || topk > num_experts)
+    return W4A16_ERR_INVALID_SHAPE;
+  if (renormalize != 0 && renormalize != 1) return W4A16_ERR_INVALID_SHAPE;
+  if (M > 0 && ld_logits < num_experts) return W4A16_ERR_INVALID_SHAPE;
+  if (M > (int64_t)INT_MAX / topk) return W4A16_ERR_INVALID_SHAPE;
+  if (M == 0) return W4A16_OK;
+  if (!logits || !topk_weights || !topk_ids) return W4A16_ERR_NULL_POINTER;
+  const uintptr_t elt = logits_dtype == W4A16_LOGITS_BF16 ? 2 : 4;
+  if ((uintptr_t)logits % elt || (uintptr_t)topk_weights % 4 || (uintptr_t)topk_ids % 4)
+    return W4A16_ERR_MISALIGNED;
+  RouterLaunch r{};
+  r.logits = logits;
+  r.ld = ld_logits;
+  r.M = M;
+  r.E = (int32_t)num_experts;
+  r.topk = (int32_t)topk;
+  r.bf16 = logits_dtype == W4A16_LOGITS_BF16;
+  r.renormalize = renormalize;
+  r.weights = topk_weights;
+  r.ids = topk_ids;
+  (void)hipGetLastError();
+  return launch_router(r, static_cast<hipStream_t>(stream)) == hipSuccess ? W4A16_OK
+                                                                         : W4A16_ERR_HIP;
 }
 
 }  // extern "C"

@@ -193,4 +193,17 @@ struct CombineLaunch {
 };
 hipError_t launch_combine(const CombineLaunch& a, hipStream_t stream);
 
+struct RouterLaunch {
+  const void* logits;  // [M, ld] fp32 or bf16
+  int64_t ld;          // row stride in elements
+  int64_t M;
+  int32_t E;           // 1..1024
+  int32_t topk;        // 1..min(64, E)
+  int32_t bf16;        // logits are bf16
+  int32_t renormalize; // 1: softmax over the selected logits; 0: over all E
+  float* weights;      // [M, topk]
+  int32_t* ids;        // [M, topk]
+};
+hipError_t launch_router(const RouterLaunch& a, hipStream_t stream);
+
 }  // namespace w4a16

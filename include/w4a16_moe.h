@@ -49,6 +49,7 @@ extern "C" {
 #define W4A16_ERR_MISALIGNED          5  /* pointer / row stride alignment    */
 #define W4A16_ERR_INVALID_BLOCK       6  /* block_size < 1                    */
 #define W4A16_ERR_HIP                 7  /* a HIP runtime call failed         */
+#define W4A16_ERR_UNSUPPORTED_DTYPE   8  /* router logits not fp32 or bf16    */
 
 /* Indices of w4a16_moe_workspace_layout()'s offsets array. */
 #define W4A16_WS_SORTED_IDS   0  /* int32 [EM]            sorted token-slot ids   */
@@ -182,6 +183,31 @@ int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
  */
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
                             void* stream);
+
+/* ---- router step (the MoE layer's left neighbour) ----------------------- */
+#define W4A16_LOGITS_F32      0
+#define W4A16_LOGITS_BF16     1
+#define W4A16_ROUTER_MAX_TOPK 64
+
+/*
+ * Top-k expert selection and weights from router logits [M, E] (row stride
+ * ld_logits elements, fp32 or bf16).
+ * Replaces the routing of make_routing, bench/bench_moe.py:225-230:
+ *   vals, ids = torch.topk(logits, k);  weights = torch.softmax(vals)
+ * topk_ids[M, topk] int32 holds each row's experts by descending logit, equal
+ * logits in ascending expert index (torch.topk leaves that order
+ * unspecified); NaN ranks above +inf and -0.0 equals +0.0, as in torch.topk.
+ * renormalize = 1: topk_weights[M, topk] fp32 = softmax over the k selected
+ * logits (the reference).  renormalize = 0: the softmax over all E logits,
+ * read at the selected experts.
+ * Requirements: 1 <= E <= 1024, 1 <= topk <= min(64, E), ld_logits >= E.
+ * One kernel launch on `stream`; M = 0 launches nothing.
+ */
+int w4a16_moe_router_topk_softmax(const void* logits, int logits_dtype,
+                                  int64_t ld_logits, int64_t M,
+                                  int64_t num_experts, int64_t topk,
+                                  int renormalize, float* topk_weights,
+                                  int32_t* topk_ids, void* stream);
 
 /* Human-readable text of a status code (static storage). */
 const char* w4a16_moe_strerror(int status);

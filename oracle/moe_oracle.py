@@ -28,6 +28,14 @@ Contents and what pins each one (the checks live in tests/test_oracle.py):
   inside (it is the timed CPU baseline).  Pinned by a float64 brute force
   (``moe_bruteforce_f64``) on tiny shapes and by linearity/zero-routing cases.
 
+* ``router_topk_softmax`` -- bench/bench_moe.py:225-230 (``torch.topk`` then
+  ``torch.softmax`` over the selected logits), equal logits in ascending
+  expert index.  Pinned by torch.topk itself on tie-free rows, by the stable
+  ``torch.sort`` on rows full of ties (torch.topk's own order among equal
+  values is unspecified and differs), by torch.topk's placement of NaN, +-inf
+  and signed zeros, by ``torch.softmax`` and by closed forms (equal logits
+  give 1/k, two logits give the logistic function).
+
 Synthetic inputs are built by the product's own generator; the oracle only
 consumes tensors.
 """
@@ -365,6 +373,43 @@ def moe_bruteforce_f64(hidden_f32: np.ndarray, w13_deq: np.ndarray, w2_deq: np.n
                 out[m, k] += float(topk_weights[m, t]) * sum(
                     float(w2_deq[e, k, n]) * a[n] for n in range(N))
     return out
+
+
+# ---------------------------------------------------------------------------
+# router step (bench/bench_moe.py:225-230)
+# ---------------------------------------------------------------------------
+
+
+def router_topk_softmax(logits, topk: int, renormalize: bool = True):
+    """(weights float64 [M, topk], ids int64 [M, topk]) from fp32 logits [M, E].
+
+    Selection: ``torch.topk(logits, topk)`` (bench_moe.py:227) -- descending
+    value, NaN first, -0.0 equal to +0.0; equal values in ascending index.
+    Weights: ``torch.softmax(vals)`` over the selected logits
+    (bench_moe.py:231), evaluated in float64; renormalize=False gives the
+    softmax over all E logits read at the selected experts instead.
+    """
+    x = np.asarray(logits, dtype=np.float32)
+    M, E = x.shape
+    if M == 0:
+        return np.zeros((0, topk)), np.zeros((0, topk), dtype=np.int64)
+    xd = x.astype(np.float64)
+    nan = np.isnan(xd)
+    # rank key: NaN above everything, then by value (-0.0 == +0.0 in float compare)
+    rank = np.where(nan, np.inf, xd)
+    ids = np.empty((M, topk), dtype=np.int64)
+    for m in range(M):
+        order = sorted(range(E), key=lambda j: (not nan[m, j], -rank[m, j], j))
+        ids[m] = order[:topk]
+    vals = np.take_along_axis(xd, ids, axis=1)
+    mx = vals[:, :1]
+    with np.errstate(invalid="ignore"):  # inf - inf and NaN rows give NaN, as in torch
+        ex = np.exp(vals - mx)
+        if renormalize:
+            den = ex.sum(axis=1, keepdims=True)
+        else:
+            den = np.exp(xd - mx).sum(axis=1, keepdims=True)
+        return ex / den, ids
 
 
 # ---------------------------------------------------------------------------

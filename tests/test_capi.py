@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 def test_abi_version_and_strerror(lib, pkg):
     assert lib.w4a16_moe_abi_version() == 1
-    for code in range(8):
+    for code in range(9):
         assert pkg._lib.strerror(code)
     assert pkg._lib.strerror(99) == "unknown status"
 
