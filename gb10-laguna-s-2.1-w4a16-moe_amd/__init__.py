@@ -20,6 +20,16 @@ from .w4a16_moe import (  # noqa: F401
     workspace_tensor,
 )
 from .routing import router_topk_softmax  # noqa: F401
+from .checkpoint import (  # noqa: F401
+    CheckpointError,
+    MoELayerWeights,
+    list_moe_layers,
+    load_moe_layer,
+    save_moe_layer,
+)
+from .layer import W4A16MoELayer  # noqa: F401
+from . import integration  # noqa: F401
 
 __all__ = ["fused_experts_w4a16", "repack_weights", "moe_align_block_size", "is_repacked",
-           "router_topk_softmax"]
+           "router_topk_softmax", "load_moe_layer", "save_moe_layer", "list_moe_layers",
+           "W4A16MoELayer", "integration"]
