@@ -18,7 +18,8 @@ several times over); W warmup calls, then exactly K timed calls bracketed by
 device synchronisation and events on the capturing stream.
 
 Per-kernel durations come from replaying graphs of one stage at a time
-(w4a16_moe_run_stage) over the same sets, timed with events on the stream the
+(w4a16_moe_run_stage_ex, with the dispatch tuning the call itself uses) over
+the same sets, timed with events on the stream the
 kernels run on; the dominant kernel's algorithmic bytes / duration is the
 roofline "achieved" figure.
 
@@ -89,6 +90,9 @@ class Workload:
                                         bias_seed=0)
             self.sets.append((x, tw, ti))
         self.touched = [synth.touched_experts(s[2], E) for s in self.sets]
+        # the dispatch choices fused_experts_w4a16 makes for this M (tuned
+        # table entry when one exists for the device, else built-in)
+        self.tuning = pkg.tuning.select(M, E, shape.N, shape.K, shape.group, dev)
         self.bytes = [n * shape.bytes_per_expert for n in self.touched]
         self.w13_bytes = [n * shape.w13_bytes_per_expert for n in self.touched]
         self.w2_bytes = [n * shape.w2_bytes_per_expert for n in self.touched]
@@ -154,7 +158,9 @@ class Workload:
         lib = self.pkg._lib.lib()
         L = self.pkg._lib
         shape, M = self.shape, self.cfg.M
-        ws_bytes = L.workspace_size(M, shape.topk, shape.E, shape.N, shape.K, shape.group)
+        ts = None if self.tuning is None else self.tuning.to_struct()
+        tptr = None if ts is None else ctypes.byref(ts)
+        ws_bytes = L.workspace_size_ex(M, shape.topk, shape.E, shape.N, shape.K, shape.group, ts)
         wss = [torch.empty(ws_bytes, dtype=torch.uint8, device=self.dev) for _ in self.sets]
         outs = [torch.empty(M, shape.K, dtype=torch.bfloat16, device=self.dev)
                 for _ in self.sets]
@@ -168,7 +174,7 @@ class Workload:
                     torch.cuda.current_stream().cuda_stream)
 
         for i in range(len(self.sets)):
-            L.check(lib.w4a16_moe_fused_experts(*args(i)))
+            L.check(lib.w4a16_moe_fused_experts_ex(*args(i), tptr))
         torch.cuda.synchronize()
         result = {}
         for stage, name in enumerate(STAGES):
@@ -177,11 +183,11 @@ class Workload:
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
                 for i in range(len(self.sets)):
-                    L.check(lib.w4a16_moe_run_stage(stage, *args(i)))
+                    L.check(lib.w4a16_moe_run_stage_ex(stage, *args(i), tptr))
             torch.cuda.current_stream().wait_stream(s)
             with torch.cuda.graph(g):
                 for i in range(len(self.sets)):
-                    L.check(lib.w4a16_moe_run_stage(stage, *args(i)))
+                    L.check(lib.w4a16_moe_run_stage_ex(stage, *args(i), tptr))
             g.replay()
             torch.cuda.synchronize()
             start = torch.cuda.Event(enable_timing=True)
@@ -246,6 +252,7 @@ def summarize(wl, t, stages):
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "TFLOP_s": round(tflops, 3),
         "pct_bf16_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 3),
+        "tuning": "built-in" if wl.tuning is None else wl.tuning.to_dict(),
     }
     if stages is not None:
         row["stage_us"] = {k: round(v * 1e3, 3) for k, v in stages.items()}

@@ -29,7 +29,9 @@ from .checkpoint import (  # noqa: F401
 )
 from .layer import W4A16MoELayer  # noqa: F401
 from . import integration  # noqa: F401
+from . import tuning  # noqa: F401
+from .tuning import Tuning  # noqa: F401
 
 __all__ = ["fused_experts_w4a16", "repack_weights", "moe_align_block_size", "is_repacked",
            "router_topk_softmax", "load_moe_layer", "save_moe_layer", "list_moe_layers",
-           "W4A16MoELayer", "integration"]
+           "W4A16MoELayer", "integration", "tuning", "Tuning"]

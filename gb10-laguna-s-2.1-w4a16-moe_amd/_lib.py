@@ -25,6 +25,7 @@ W4A16_ERR_MISALIGNED = 5
 W4A16_ERR_INVALID_BLOCK = 6
 W4A16_ERR_HIP = 7
 W4A16_ERR_UNSUPPORTED_DTYPE = 8
+W4A16_ERR_INVALID_TUNING = 9
 
 LOGITS_F32 = 0
 LOGITS_BF16 = 1
@@ -42,7 +43,7 @@ WS_NFIELDS = 8
 
 FUSED_BLOCK_M = 16
 GEMV_MAX_TOKENS = 4
-GEMV_ONLY_MAX_M = 16
+GEMV_ONLY_MAX_M = 24
 
 EXPORTED_SYMBOLS = (
     "w4a16_moe_align_sizes",
@@ -54,6 +55,10 @@ EXPORTED_SYMBOLS = (
     "w4a16_moe_run_stage",
     "w4a16_moe_dropped_pairs",
     "w4a16_moe_router_topk_softmax",
+    "w4a16_moe_default_tuning",
+    "w4a16_moe_workspace_size_ex",
+    "w4a16_moe_fused_experts_ex",
+    "w4a16_moe_run_stage_ex",
     "w4a16_moe_strerror",
     "w4a16_moe_abi_version",
 )
@@ -66,6 +71,14 @@ _lib: ctypes.CDLL | None = None
 
 class LibraryNotBuilt(RuntimeError):
     pass
+
+
+class TuningStruct(ctypes.Structure):
+    """struct w4a16_moe_tuning (include/w4a16_moe.h)."""
+
+    _fields_ = [("gemv_only_max_m", ctypes.c_int32), ("gemv_max_tokens", ctypes.c_int32),
+                ("gemv_tokens_per_pass", ctypes.c_int32), ("mfma_tile_m", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 4)]
 
 
 def _declare(lib: ctypes.CDLL) -> None:
@@ -95,6 +108,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.w4a16_moe_run_stage.argtypes = [ctypes.c_int] + fused
     lib.w4a16_moe_dropped_pairs.restype = ctypes.c_int
     lib.w4a16_moe_dropped_pairs.argtypes = [_vp, ctypes.POINTER(ctypes.c_int32), _vp]
+    tp = ctypes.POINTER(TuningStruct)
+    lib.w4a16_moe_default_tuning.restype = ctypes.c_int
+    lib.w4a16_moe_default_tuning.argtypes = [_i64] * 6 + [tp]
+    lib.w4a16_moe_workspace_size_ex.restype = ctypes.c_int
+    lib.w4a16_moe_workspace_size_ex.argtypes = [_i64] * 6 + [tp, ctypes.POINTER(ctypes.c_size_t)]
+    lib.w4a16_moe_fused_experts_ex.restype = ctypes.c_int
+    lib.w4a16_moe_fused_experts_ex.argtypes = fused + [tp]
+    lib.w4a16_moe_run_stage_ex.restype = ctypes.c_int
+    lib.w4a16_moe_run_stage_ex.argtypes = [ctypes.c_int] + fused + [tp]
     lib.w4a16_moe_router_topk_softmax.restype = ctypes.c_int
     lib.w4a16_moe_router_topk_softmax.argtypes = [
         _vp, ctypes.c_int, _i64, _i64, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]
@@ -136,6 +158,20 @@ def workspace_size(M: int, topk: int, E: int, N: int, K: int, group: int) -> int
     out = ctypes.c_size_t()
     check(lib().w4a16_moe_workspace_size(M, topk, E, N, K, group, ctypes.byref(out)))
     return out.value
+
+
+def workspace_size_ex(M: int, topk: int, E: int, N: int, K: int, group: int,
+                      tuning: "TuningStruct | None") -> int:
+    out = ctypes.c_size_t()
+    ptr = ctypes.byref(tuning) if tuning is not None else None
+    check(lib().w4a16_moe_workspace_size_ex(M, topk, E, N, K, group, ptr, ctypes.byref(out)))
+    return out.value
+
+
+def default_tuning(M: int, topk: int, E: int, N: int, K: int, group: int) -> TuningStruct:
+    t = TuningStruct()
+    check(lib().w4a16_moe_default_tuning(M, topk, E, N, K, group, ctypes.byref(t)))
+    return t
 
 
 def workspace_layout(M: int, topk: int, E: int, N: int, K: int, group: int) -> list[int]:

@@ -33,6 +33,14 @@ int align_sizes(int64_t M, int64_t topk, int64_t E, int64_t block, int64_t* em,
   return W4A16_OK;
 }
 
+// Dispatch choices of one call: the public w4a16_moe_tuning, resolved.
+struct Tuning {
+  int gemv_only_max_m;  // M at or below this: every expert on the GEMV kernels
+  int gemv_max_tokens;  // above it: experts with more pairs go to MFMA tiles
+  int tc;               // GEMV token rows per pass (0 = launcher's choice)
+  int tile_m;           // MFMA tile height
+};
+
 struct Layout {
   size_t off[W4A16_WS_NFIELDS];
   size_t total;
@@ -43,6 +51,8 @@ struct Layout {
   int64_t max_tiles;  // bound of the MFMA tile list
   int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
   int64_t max_items;  // bound of the self-routed work items (experts)
+  int gemv_max_tokens;
+  int tc;
 };
 
 // An expert with more than this many (token, slot) pairs runs on MFMA tiles;
@@ -60,8 +70,28 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   return W4A16_OK;
 }
 
+Tuning default_tuning() { return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM}; }
+
+// NULL selects the built-in choices; reserved fields must be zero.
+int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
+  *out = default_tuning();
+  if (!t) return W4A16_OK;
+  for (int i = 0; i < 4; ++i)
+    if (t->reserved[i] != 0) return W4A16_ERR_INVALID_TUNING;
+  if (t->gemv_only_max_m < 0) return W4A16_ERR_INVALID_TUNING;
+  if (t->gemv_max_tokens < 0 || t->gemv_max_tokens >= W4A16_FUSED_BLOCK_M)
+    return W4A16_ERR_INVALID_TUNING;
+  const int tc = t->gemv_tokens_per_pass;
+  if (tc != 0 && tc != 1 && tc != 2 && tc != 4) return W4A16_ERR_INVALID_TUNING;
+  if (t->mfma_tile_m != 0 && t->mfma_tile_m != kMfmaTileM) return W4A16_ERR_INVALID_TUNING;
+  out->gemv_only_max_m = t->gemv_only_max_m;
+  out->gemv_max_tokens = t->gemv_max_tokens;
+  out->tc = tc;
+  return W4A16_OK;
+}
+
 int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
-                   int64_t group, Layout* L) {
+                   int64_t group, const Tuning& T, Layout* L) {
   int st = check_gemm_shape(N, K, group);
   if (st) return st;
   st = align_sizes(M, topk, E, W4A16_FUSED_BLOCK_M, &L->em, &L->nb);
@@ -70,17 +100,17 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // MFMA tiles need whole 256-row weight tiles and whole 256-element weight
   // slabs on both GEMMs; small batches cannot give an expert enough pairs to
   // pay for the extra launches.
-  L->mfma = M > kGemvOnlyMaxM && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
-  const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (kGemvMaxTokens + 1));
-  // 256-slot tiles once an average expert holds more than 128 pairs: the
-  // whole expert then shares one dequantization of its weights.
-  L->tile_m = kMfmaTileM;
+  L->mfma = M > T.gemv_only_max_m && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
+  L->gemv_max_tokens = T.gemv_max_tokens;
+  L->tc = T.tc;
+  const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (T.gemv_max_tokens + 1));
+  L->tile_m = T.tile_m;
   L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
                         : std::min<int64_t>((int64_t)n_tok, L->nb);
   // Small batches: the GEMV kernels route themselves from topk_ids (work
   // item = one routed expert), so the align kernel is not run.
-  L->route = !L->mfma && M >= 1 && M <= kGemvOnlyMaxM &&
+  L->route = !L->mfma && M >= 1 && M <= T.gemv_only_max_m &&
              gemv_route_fits((int)n_tok, (int)E, (int)K, (int)N);
   L->max_items = L->route ? std::min<int64_t>(E, (int64_t)n_tok) : 0;
   size_t cur = 0;
@@ -116,10 +146,14 @@ struct FusedArgs {
   int64_t ld_out;
   void* ws;
   size_t ws_bytes;
+  const w4a16_moe_tuning* tuning;  // null: built-in choices
 };
 
 int validate(const FusedArgs& a, Layout* L) {
-  int st = compute_layout(a.M, a.topk, a.E, a.N, a.K, a.group, L);
+  Tuning T;
+  int st = resolve_tuning(a.tuning, &T);
+  if (st) return st;
+  st = compute_layout(a.M, a.topk, a.E, a.N, a.K, a.group, T, L);
   if (st) return st;
   if (a.M == 0) return W4A16_OK;
   if (!a.hidden || !a.w13 || !a.w2 || !a.s13 || !a.s2 || !a.topk_w || !a.ids ||
@@ -173,7 +207,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
     al.n_tiles = header + 2;
     al.gemv_blocks = gemv_blocks;
     al.n_gemv = header + 3;
-    al.gemv_max_tokens = kGemvMaxTokens;
+    al.gemv_max_tokens = L.gemv_max_tokens;
     al.tile_m = L.tile_m;
   }
   if (want(0) && !L.route && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
@@ -190,6 +224,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.group = (int32_t)a.group;
   g.max_blocks = (int32_t)L.max_gemv;
   g.num_experts = (int32_t)a.E;
+  g.tc = L.tc;
   if (L.route) {
     g.ids = a.ids;
     g.max_items = (int32_t)L.max_items;
@@ -282,6 +317,7 @@ const char* w4a16_moe_strerror(int status) {
     case W4A16_ERR_INVALID_BLOCK: return "invalid block_size";
     case W4A16_ERR_HIP: return "HIP runtime error";
     case W4A16_ERR_UNSUPPORTED_DTYPE: return "unsupported logits dtype";
+    case W4A16_ERR_INVALID_TUNING: return "invalid tuning value";
     default: return "unknown status";
   }
 }
@@ -324,14 +360,39 @@ int w4a16_moe_align_block_size(const int32_t* topk_ids, int64_t M, int64_t topk,
                                                                          : W4A16_ERR_HIP;
 }
 
-int w4a16_moe_workspace_size(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
-                             int64_t K, int64_t group_size, size_t* bytes) {
-  if (!bytes) return W4A16_ERR_NULL_POINTER;
+int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                             int64_t K, int64_t group_size, w4a16_moe_tuning* tuning) {
+  if (!tuning) return W4A16_ERR_NULL_POINTER;
   Layout L;
-  const int st = compute_layout(M, topk, num_experts, N, K, group_size, &L);
+  const Tuning T = default_tuning();
+  const int st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L);
+  if (st) return st;
+  *tuning = w4a16_moe_tuning{};
+  tuning->gemv_only_max_m = T.gemv_only_max_m;
+  tuning->gemv_max_tokens = T.gemv_max_tokens;
+  tuning->gemv_tokens_per_pass = T.tc;
+  tuning->mfma_tile_m = T.tile_m;
+  return W4A16_OK;
+}
+
+int w4a16_moe_workspace_size_ex(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                                int64_t K, int64_t group_size,
+                                const w4a16_moe_tuning* tuning, size_t* bytes) {
+  if (!bytes) return W4A16_ERR_NULL_POINTER;
+  Tuning T;
+  int st = resolve_tuning(tuning, &T);
+  if (st) return st;
+  Layout L;
+  st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L);
   if (st) return st;
   *bytes = L.total;
   return W4A16_OK;
+}
+
+int w4a16_moe_workspace_size(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                             int64_t K, int64_t group_size, size_t* bytes) {
+  return w4a16_moe_workspace_size_ex(M, topk, num_experts, N, K, group_size, nullptr,
+                                     bytes);
 }
 
 int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
@@ -339,10 +400,27 @@ int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts, int
                                size_t offsets[W4A16_WS_NFIELDS]) {
   if (!offsets) return W4A16_ERR_NULL_POINTER;
   Layout L;
-  const int st = compute_layout(M, topk, num_experts, N, K, group_size, &L);
+  const int st = compute_layout(M, topk, num_experts, N, K, group_size, default_tuning(), &L);
   if (st) return st;
   for (int i = 0; i < W4A16_WS_NFIELDS; ++i) offsets[i] = L.off[i];
   return W4A16_OK;
+}
+
+int w4a16_moe_fused_experts_ex(const void* hidden, int64_t ld_hidden,
+                               const void* w13_packed, const void* w2_packed,
+                               const void* w13_scale, const void* w2_scale,
+                               const float* topk_weights, const int32_t* topk_ids,
+                               int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                               int64_t K, int64_t group_size, void* out, int64_t ld_out,
+                               void* workspace, size_t workspace_bytes, void* stream,
+                               const w4a16_moe_tuning* tuning) {
+  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
+                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
+                    out, ld_out, workspace, workspace_bytes, tuning};
+  Layout L;
+  const int st = validate(a, &L);
+  if (st || M == 0) return st;
+  return run_fused(a, L, static_cast<hipStream_t>(stream), nullptr);
 }
 
 int w4a16_moe_fused_experts(const void* hidden, int64_t ld_hidden, const void* w13_packed,
@@ -352,13 +430,10 @@ int w4a16_moe_fused_experts(const void* hidden, int64_t ld_hidden, const void* w
                             int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
                             void* out, int64_t ld_out, void* workspace,
                             size_t workspace_bytes, void* stream) {
-  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
-                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
-                    out, ld_out, workspace, workspace_bytes};
-  Layout L;
-  const int st = validate(a, &L);
-  if (st || M == 0) return st;
-  return run_fused(a, L, static_cast<hipStream_t>(stream), nullptr);
+  return w4a16_moe_fused_experts_ex(hidden, ld_hidden, w13_packed, w2_packed, w13_scale,
+                                    w2_scale, topk_weights, topk_ids, M, topk, num_experts,
+                                    N, K, group_size, out, ld_out, workspace,
+                                    workspace_bytes, stream, nullptr);
 }
 
 int w4a16_moe_fused_experts_profiled(
@@ -370,7 +445,7 @@ int w4a16_moe_fused_experts_profiled(
   if (!stage_ms) return W4A16_ERR_NULL_POINTER;
   const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
                     topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
-                    out, ld_out, workspace, workspace_bytes};
+                    out, ld_out, workspace, workspace_bytes, nullptr};
   Layout L;
   int st = validate(a, &L);
   if (st) return st;
@@ -398,6 +473,24 @@ int w4a16_moe_fused_experts_profiled(
   return st;
 }
 
+int w4a16_moe_run_stage_ex(int stage, const void* hidden, int64_t ld_hidden,
+                           const void* w13_packed, const void* w2_packed,
+                           const void* w13_scale, const void* w2_scale,
+                           const float* topk_weights, const int32_t* topk_ids, int64_t M,
+                           int64_t topk, int64_t num_experts, int64_t N, int64_t K,
+                           int64_t group_size, void* out, int64_t ld_out, void* workspace,
+                           size_t workspace_bytes, void* stream,
+                           const w4a16_moe_tuning* tuning) {
+  if (stage < 0 || stage > 3) return W4A16_ERR_INVALID_SHAPE;
+  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
+                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
+                    out, ld_out, workspace, workspace_bytes, tuning};
+  Layout L;
+  const int st = validate(a, &L);
+  if (st || M == 0) return st;
+  return run_fused(a, L, static_cast<hipStream_t>(stream), nullptr, stage);
+}
+
 int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
                         const void* w13_packed, const void* w2_packed,
                         const void* w13_scale, const void* w2_scale,
@@ -405,14 +498,10 @@ int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
                         int64_t topk, int64_t num_experts, int64_t N, int64_t K,
                         int64_t group_size, void* out, int64_t ld_out, void* workspace,
                         size_t workspace_bytes, void* stream) {
-  if (stage < 0 || stage > 3) return W4A16_ERR_INVALID_SHAPE;
-  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
-                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
-                    out, ld_out, workspace, workspace_bytes};
-  Layout L;
-  const int st = validate(a, &L);
-  if (st || M == 0) return st;
-  return run_fused(a, L, static_cast<hipStream_t>(stream), nullptr, stage);
+  return w4a16_moe_run_stage_ex(stage, hidden, ld_hidden, w13_packed, w2_packed, w13_scale,
+                                w2_scale, topk_weights, topk_ids, M, topk, num_experts, N,
+                                K, group_size, out, ld_out, workspace, workspace_bytes,
+                                stream, nullptr);
 }
 
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count, void* stream) {

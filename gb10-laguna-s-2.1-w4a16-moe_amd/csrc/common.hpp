@@ -154,6 +154,8 @@ struct GemvLaunch {
   const int32_t* ids;      // [n_tok] topk_ids
   int32_t max_items;       // grid bound of the number of routed experts
   int32_t* dropped_out;    // w13: [1] pairs with ids outside [0, E)
+  int32_t tc;              // token rows per pass: 0 = chosen by the launcher,
+                           // else 1, 2 or 4 (lowered while LDS does not fit)
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);

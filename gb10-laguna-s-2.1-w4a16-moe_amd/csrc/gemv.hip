@@ -512,10 +512,16 @@ size_t route_bytes(const GemvLaunch& a) {
 // get one or two pairs; beyond that stage four rows per pass.
 int pick_tc(const GemvLaunch& a, int num_experts) {
   const int M = a.n_tok / a.topk;
+  // Measured on MI355X (E=256, top-10): from M = 8 up, four token rows per
+  // pass let the experts with 3-4 pairs finish in one pass (M=16: 137 vs
+  // 141 us uniform, 105 vs 120 us skewed routing).
+  (void)num_experts;
   int tc = 4;
-  if (M <= 1)
+  if (a.tc > 0)
+    tc = a.tc;
+  else if (M <= 1)
     tc = 1;
-  else if (a.n_tok <= num_experts)
+  else if (M < 8)
     tc = 2;
   while (tc > 1 && gemv_lds_bytes(tc, a.kdim) + route_bytes(a) > kMaxLds) tc >>= 1;
   return tc;

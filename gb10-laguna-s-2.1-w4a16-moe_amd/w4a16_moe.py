@@ -25,6 +25,7 @@ import threading
 import torch
 
 from . import _lib
+from . import tuning as _tuning
 
 _GROUP_SIZE_DEFAULT = 32
 # Accepted for signature compatibility with the reference; the HIP kernels
@@ -148,11 +149,12 @@ def _packed_cols(w: torch.Tensor) -> int:
 
 
 def _workspace(device: torch.device, M: int, topk: int, E: int, N: int, K: int,
-               group: int) -> torch.Tensor:
-    key = (str(device), M, topk, E, N, K, group)
+               group: int, tuning: "_tuning.Tuning | None" = None) -> torch.Tensor:
+    key = (str(device), M, topk, E, N, K, group, tuning)
     ws = _WS_CACHE.get(key)
     if ws is None:
-        nbytes = _lib.workspace_size(M, topk, E, N, K, group)
+        ts = None if tuning is None else tuning.to_struct()
+        nbytes = _lib.workspace_size_ex(M, topk, E, N, K, group, ts)
         with _WS_LOCK:
             ws = _WS_CACHE.get(key)
             if ws is None:
@@ -163,7 +165,7 @@ def _workspace(device: torch.device, M: int, topk: int, E: int, N: int, K: int,
 
 class _Prepared:
     __slots__ = ("hidden", "w1_q", "w2_q", "w1_scale", "w2_scale", "topk_weights",
-                 "topk_ids", "M", "K", "N", "E", "topk", "group", "device")
+                 "topk_ids", "M", "K", "N", "E", "topk", "group", "device", "tuning")
 
 
 def _prepare(hidden, w1_q, w2_q, w1_scale, w2_scale, topk_weights, topk_ids,
@@ -219,7 +221,21 @@ def _prepare(hidden, w1_q, w2_q, w1_scale, w2_scale, topk_weights, topk_ids,
         tw = tw.to(torch.float32)
     p.topk_weights = tw.contiguous()
     p.topk_ids = _ids_i32(topk_ids)
+    p.tuning = None
     return p
+
+
+def _tuning_for(p: _Prepared, tuning) -> None:
+    """Explicit tuning, else the device table's entry for M, else built-in."""
+    if tuning is None:
+        tuning = _tuning.select(p.M, p.E, p.N, p.K, p.group, p.device)
+    elif not isinstance(tuning, _tuning.Tuning):
+        _fail("tuning must be a tuning.Tuning")
+    p.tuning = tuning
+
+
+def _tuning_ptr(p: _Prepared):
+    return None if p.tuning is None else ctypes.byref(p.tuning.to_struct())
 
 
 def _fused_args(p: _Prepared, out: torch.Tensor, ws: torch.Tensor):
@@ -243,6 +259,7 @@ def fused_experts_w4a16(
     block_m: int = BLOCK_M,
     block_n: int = BLOCK_N,
     block_k: int = BLOCK_K,
+    tuning: "_tuning.Tuning | None" = None,
 ) -> torch.Tensor:
     """Fused W4A16 grouped-MoE experts (w13 + SiLU-mul + w2 + top-k sum).
 
@@ -257,6 +274,9 @@ def fused_experts_w4a16(
     topk_ids      [M, topk] expert ids (int32; int64 is cast).
     group_size    symmetric int4 group size along the reduction axis (32/64/128).
     block_m, block_n, block_k: accepted for compatibility, not used.
+    tuning        dispatch choices (tuning.Tuning); default: the device's tuned
+                  table entry nearest to M if a table exists, else the
+                  library's built-in choices.
 
     Returns a new [M, K] bf16 tensor.  All work is enqueued on the current
     stream with no host synchronisation (HIP-graph capturable once the
@@ -268,9 +288,10 @@ def fused_experts_w4a16(
     out = torch.empty((p.M, p.K), dtype=torch.bfloat16, device=p.device)
     if p.M == 0:
         return out
-    ws = _workspace(p.device, p.M, p.topk, p.E, p.N, p.K, p.group)
+    _tuning_for(p, tuning)
+    ws = _workspace(p.device, p.M, p.topk, p.E, p.N, p.K, p.group, p.tuning)
     with torch.cuda.device(p.device):
-        st = _lib.lib().w4a16_moe_fused_experts(*_fused_args(p, out, ws))
+        st = _lib.lib().w4a16_moe_fused_experts_ex(*_fused_args(p, out, ws), _tuning_ptr(p))
     _lib.check(st)
     return out
 
@@ -296,13 +317,17 @@ def fused_experts_w4a16_profiled(hidden, w1_q, w2_q, w1_scale, w2_scale, topk_we
 
 
 def workspace_tensor(hidden: torch.Tensor, topk_ids: torch.Tensor, w1_q: torch.Tensor,
-                     w2_q: torch.Tensor, group_size: int = _GROUP_SIZE_DEFAULT):
-    """The cached workspace of a shape and its field offsets (for inspection)."""
+                     w2_q: torch.Tensor, group_size: int = _GROUP_SIZE_DEFAULT,
+                     tuning: "_tuning.Tuning | None" = None):
+    """The cached workspace fused_experts_w4a16 uses for this shape (and tuning,
+    chosen as that call chooses it), with the built-in layout's field offsets."""
     M, K = hidden.shape
     topk = topk_ids.shape[1]
     E = w1_q.shape[0]
     N = w1_q.shape[1] // 2
-    ws = _workspace(hidden.device, M, topk, E, N, K, group_size)
+    if tuning is None:
+        tuning = _tuning.select(M, E, N, K, group_size, hidden.device)
+    ws = _workspace(hidden.device, M, topk, E, N, K, group_size, tuning)
     return ws, _lib.workspace_layout(M, topk, E, N, K, group_size)
 
 

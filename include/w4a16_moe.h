@@ -50,6 +50,7 @@ extern "C" {
 #define W4A16_ERR_INVALID_BLOCK       6  /* block_size < 1                    */
 #define W4A16_ERR_HIP                 7  /* a HIP runtime call failed         */
 #define W4A16_ERR_UNSUPPORTED_DTYPE   8  /* router logits not fp32 or bf16    */
+#define W4A16_ERR_INVALID_TUNING      9  /* a w4a16_moe_tuning field out of range */
 
 /* Indices of w4a16_moe_workspace_layout()'s offsets array. */
 #define W4A16_WS_SORTED_IDS   0  /* int32 [EM]            sorted token-slot ids   */
@@ -76,10 +77,10 @@ extern "C" {
  * run on the GEMV kernels. */
 #define W4A16_GEMV_MAX_TOKENS 4
 
-/* Calls with at most this many tokens run every expert on the GEMV kernels:
- * no expert can then hold more than one 16-slot block, and the MFMA
- * launches would only add their fixed cost. */
-#define W4A16_GEMV_ONLY_MAX_M 16
+/* Calls with at most this many tokens run every expert on the GEMV kernels
+ * (by default; see w4a16_moe_tuning): few experts then hold more than a
+ * handful of pairs, and the MFMA launches would only add their fixed cost. */
+#define W4A16_GEMV_ONLY_MAX_M 24
 
 /*
  * Sizes of moe_align_block_size's outputs.
@@ -183,6 +184,71 @@ int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
  */
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
                             void* stream);
+
+/* ---- dispatch tuning (the per-M tile selector) -------------------------- */
+/*
+ * How a call splits its work between the kernels.  The analogue of the
+ * reference's tuned per-M kernel configurations: its fused_experts_w4a16
+ * takes block_m/block_n/block_k (kernels/w4a16_moe.py:678-690) and the stock
+ * path reads them from a per-device JSON keyed by M
+ * (configs/E=256,N=1024,device_name=NVIDIA_GB10,dtype=int4_w4a16.json,
+ * written by bench/tune_configs.py).  Here the tile shapes are fixed per
+ * kernel and the choices are which kernels run:
+ *   gemv_only_max_m       calls with M <= this run every expert on the GEMV
+ *                         kernels (routing themselves when it fits in LDS);
+ *   gemv_max_tokens       larger calls (N, K multiples of 256) send experts
+ *                         with more (token, slot) pairs than this (0..15) to
+ *                         the MFMA kernels, the others to the GEMV kernels;
+ *   gemv_tokens_per_pass  token rows one GEMV pass reads the weights for:
+ *                         0 (the library's choice), 1, 2 or 4;
+ *   mfma_tile_m           MFMA tile height in slots: 0 (default) or 128.
+ * reserved must be zero.  Every choice computes the same function; the
+ * GEMV and MFMA kernels differ only in rounding (within the tolerance of
+ * fused_experts).  A NULL tuning selects w4a16_moe_default_tuning's values.
+ */
+typedef struct w4a16_moe_tuning {
+  int32_t gemv_only_max_m;
+  int32_t gemv_max_tokens;
+  int32_t gemv_tokens_per_pass;
+  int32_t mfma_tile_m;
+  int32_t reserved[4];
+} w4a16_moe_tuning;
+
+/* The built-in tuning for a shape (what NULL selects).  No counterpart in the
+ * reference, whose defaults live in kernels/w4a16_moe.py:686-689. */
+int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts,
+                             int64_t N, int64_t K, int64_t group_size,
+                             w4a16_moe_tuning* tuning);
+
+/* w4a16_moe_workspace_size for calls made with `tuning`. */
+int w4a16_moe_workspace_size_ex(int64_t M, int64_t topk, int64_t num_experts,
+                                int64_t N, int64_t K, int64_t group_size,
+                                const w4a16_moe_tuning* tuning, size_t* bytes);
+
+/* w4a16_moe_fused_experts with explicit dispatch choices: the block_m /
+ * block_n / block_k arguments of fused_experts_w4a16,
+ * kernels/w4a16_moe.py:686-689.  The workspace must hold
+ * w4a16_moe_workspace_size_ex(..., tuning) bytes. */
+int w4a16_moe_fused_experts_ex(const void* hidden, int64_t ld_hidden,
+                               const void* w13_packed, const void* w2_packed,
+                               const void* w13_scale, const void* w2_scale,
+                               const float* topk_weights, const int32_t* topk_ids,
+                               int64_t M, int64_t topk, int64_t num_experts,
+                               int64_t N, int64_t K, int64_t group_size,
+                               void* out, int64_t ld_out, void* workspace,
+                               size_t workspace_bytes, void* stream,
+                               const w4a16_moe_tuning* tuning);
+
+/* w4a16_moe_run_stage with explicit dispatch choices (measurement helper). */
+int w4a16_moe_run_stage_ex(int stage, const void* hidden, int64_t ld_hidden,
+                           const void* w13_packed, const void* w2_packed,
+                           const void* w13_scale, const void* w2_scale,
+                           const float* topk_weights, const int32_t* topk_ids,
+                           int64_t M, int64_t topk, int64_t num_experts,
+                           int64_t N, int64_t K, int64_t group_size, void* out,
+                           int64_t ld_out, void* workspace,
+                           size_t workspace_bytes, void* stream,
+                           const w4a16_moe_tuning* tuning);
 
 /* ---- router step (the MoE layer's left neighbour) ----------------------- */
 #define W4A16_LOGITS_F32      0

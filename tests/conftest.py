@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
@@ -12,6 +13,11 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 import __graft_entry__  # noqa: E402
+
+# Parity tests restate the library's built-in dispatch; a tuned table for the
+# device (tuning.py) would change which kernels run.  Tests of the tables
+# themselves clear this per test.
+os.environ["W4A16_MOE_TUNING"] = "default"
 
 
 def pytest_configure(config):
