@@ -50,7 +50,7 @@ struct Layout {
   int tile_m;         // MFMA tile height (slots)
   int64_t max_tiles;  // bound of the MFMA tile list
   int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
-  int64_t max_items;  // bound of the self-routed work items (experts)
+  int64_t max_items;  // self-routed work items: one per (token, slot) pair
   int gemv_max_tokens;
   int tc;
 };
@@ -112,7 +112,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // item = one routed expert), so the align kernel is not run.
   L->route = !L->mfma && M >= 1 && M <= T.gemv_only_max_m &&
              gemv_route_fits((int)n_tok, (int)E, (int)K, (int)N);
-  L->max_items = L->route ? std::min<int64_t>(E, (int64_t)n_tok) : 0;
+  L->max_items = L->route ? (int64_t)n_tok : 0;
   size_t cur = 0;
   auto put = [&](int field, size_t bytes) {
     L->off[field] = cur;

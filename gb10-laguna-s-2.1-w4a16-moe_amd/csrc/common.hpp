@@ -149,10 +149,10 @@ struct GemvLaunch {
   uint32_t nib_mask;          // set by the launcher (see gemv.hip)
   uint32_t nib_magic;
   // Self-routing (small batches, the align kernel is not run): when `ids`
-  // is set, work item i is the i-th expert with routed pairs, found by every
-  // workgroup from topk_ids itself.
+  // is set, work item i is flat slot i, which works when it is the first
+  // slot routed to its expert, found by every wave from topk_ids itself.
   const int32_t* ids;      // [n_tok] topk_ids
-  int32_t max_items;       // grid bound of the number of routed experts
+  int32_t max_items;       // work items: n_tok
   int32_t* dropped_out;    // w13: [1] pairs with ids outside [0, E)
   int32_t tc;              // token rows per pass: 0 = chosen by the launcher,
                            // else 1, 2 or 4 (lowered while LDS does not fit)

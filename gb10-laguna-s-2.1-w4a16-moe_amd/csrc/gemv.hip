@@ -107,90 +107,88 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 #define GEMV_MIN_WAVES 1
 #endif
 
-// Self-routing tables in LDS after the staged rows (ints): ids, expert
-// flags, the item's flat indices, per-wave counts and scalars.
-__host__ __device__ __forceinline__ int route_ints(int n_tok, int num_experts) {
-  return 2 * n_tok + num_experts + 24;
+// Self-routing handles at most this many (token, slot) pairs: four per lane.
+constexpr int kRouteMaxTok = 256;
+
+// Position of the k-th set bit of m (k < popcount(m)): binary search on the
+// popcount of the lower half.
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
+  int pos = 0;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    const uint64_t low = m & ((1ull << s) - 1ull);
+    const int c = __popcll(low);
+    const bool up = k >= c;
+    k -= up ? c : 0;
+    m = up ? (m >> s) : low;
+    pos += up ? s : 0;
+  }
+  return pos;
 }
 
-// Work item `item` is the item-th expert (ascending) that has routed pairs;
-// its pairs in ascending flat index are the order moe_align_block_size gives
-// them (kernels/w4a16_moe.py:243-278).  Found from topk_ids directly: fills
-// r_ids[n_tok], r_slots[0..t_out) and r_misc[17] (pairs with ids outside
-// [0, E)).  e_out = -1 when item is past the last routed expert.  All NT
-// threads must call; every exit is workgroup-uniform.
-template <int NT>
-__device__ __forceinline__ void route_expert(const GemvLaunch& a, int item, int* r_ids,
-                                             int* r_flag, int* r_slots, int* r_misc,
-                                             int& e_out, int& t_out) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wid = tid >> 6;
-  constexpr int NW = NT / 64;
+// Self-routing in registers, by every wave on its own (no LDS, no barrier).
+// Work item `item` is flat slot `item`; it carries work only when that slot
+// is the first (lowest flat index) routed to its expert, and then covers all
+// of the expert's pairs in ascending flat index -- the order
+// moe_align_block_size gives them (kernels/w4a16_moe.py:243-278).  Lane l
+// gets in fl[j] the flat index of the expert's pair of rank l + 64 j (n_tok
+// past the last).  e_out = -1 when the item has no work; dropped = pairs with
+// ids outside [0, E).  Requires 1 <= n_tok <= kRouteMaxTok.
+__device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e_out,
+                                           int& t_out, int (&fl)[4], int& dropped) {
+  const int lane = __lane_id();
   const int n_tok = a.n_tok, E = a.num_experts;
-  const uint64_t below = lanemask_lt();
-  for (int i = tid; i < E; i += NT) r_flag[i] = 0;
-  if (tid == 0) {
-    r_misc[16] = -1;
-    r_misc[17] = 0;
+  constexpr int kNone = -2147483647 - 1;
+  int id[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {  // clamped loads, all in flight together
+    const int f = lane + 64 * q;
+    const int v = a.ids[min(f, n_tok - 1)];
+    id[q] = f < n_tok ? v : kNone;
   }
-  __syncthreads();
   int drop = 0;
-  for (int f = tid; f < n_tok; f += NT) {
-    const int e = a.ids[f];
-    r_ids[f] = e;
-    if (e >= 0 && e < E)
-      r_flag[e] = 1;
-    else
-      ++drop;
-  }
-  if (drop) atomicAdd(&r_misc[17], drop);
-  __syncthreads();
-
-  // The item-th used expert: ballot counts per wave, prefix over the waves.
-  int base = 0;
-  for (int e0 = 0; e0 < E; e0 += NT) {
-    const int e = e0 + tid;
-    const bool used = e < E && r_flag[e] != 0;
-    const uint64_t b = ballot(used);
-    if (lane == 0) r_misc[wid] = __popcll(b);
-    __syncthreads();
-    int wp = 0, tot = 0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int c = r_misc[w];
-      wp += w < wid ? c : 0;
-      tot += c;
-    }
-    if (used && base + wp + __popcll(b & below) == item) r_misc[16] = e;
-    base += tot;
-    __syncthreads();
-  }
-  const int e_sel = r_misc[16];
-  e_out = e_sel;
+  for (int q = 0; q < 4; ++q)
+    drop += __popcll(ballot(id[q] != kNone && (id[q] < 0 || id[q] >= E)));
+  dropped = drop;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fl[j] = n_tok;
+  e_out = -1;
   t_out = 0;
-  if (e_sel < 0) return;
-
-  // Its pairs, ascending flat index.
-  int cnt = 0;
-  for (int f0 = 0; f0 < n_tok; f0 += NT) {
-    const int f = f0 + tid;
-    const bool hit = f < n_tok && r_ids[f] == e_sel;
-    const uint64_t b = ballot(hit);
-    if (lane == 0) r_misc[wid] = __popcll(b);
-    __syncthreads();
-    int wp = 0, tot = 0;
+  const int e = __builtin_amdgcn_readfirstlane(a.ids[item]);
+  if (e < 0 || e >= E) return;
+  bool earlier = false;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int c = r_misc[w];
-      wp += w < wid ? c : 0;
-      tot += c;
-    }
-    if (hit) r_slots[cnt + wp + __popcll(b & below)] = f;
-    cnt += tot;
-    __syncthreads();
+  for (int q = 0; q < 4; ++q) earlier |= (lane + 64 * q < item) && id[q] == e;
+  if (ballot(earlier) != 0) return;  // an earlier slot's item owns this expert
+  uint64_t m[4];
+  int c[4];
+  int T = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    m[q] = ballot(id[q] == e);
+    c[q] = __popcll(m[q]);
+    T += c[q];
   }
-  t_out = cnt;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j * 64 >= T) break;  // uniform
+    const int R = lane + 64 * j;
+    int p = 0, q_sel = 0, p_sel = 0;
+    uint64_t m_sel = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (R >= p && R < p + c[q]) {
+        q_sel = q;
+        p_sel = p;
+        m_sel = m[q];
+      }
+      p += c[q];
+    }
+    if (R < T) fl[j] = 64 * q_sel + nth_set_bit(m_sel, R - p_sel);
+  }
+  e_out = e;
+  t_out = T;
 }
 
 // MODE 0: w13 rows (gate n, up N+n), epilogue SiLU(gate)*up -> bf16 inter.
@@ -221,24 +219,21 @@ void gemv_kernel(const GemvLaunch a) {
   const int chunk = has_rows ? chunk_raw : chunks - 1;  // idle waves re-read a slab
   const int tid = threadIdx.x;
   const int lane = __lane_id();
-  const int E = a.num_experts;
 
-  // LDS: staged activation rows | their -C values | routing tables
+  // LDS: staged activation rows | their -C values
   const int G0 = a.kdim >> 5;
   const int row_oct = staged_row_octets(a.kdim);
   const int xc_pitch = G0 + 1;
   u32x4_t* xp = lds;
   float* xc = reinterpret_cast<float*>(lds + TC * row_oct);
-  int* r_ids = reinterpret_cast<int*>(xc + TC * xc_pitch);
-  int* r_flag = r_ids + a.n_tok;
-  int* r_slots = r_flag + E;
-  int* r_misc = r_slots + a.n_tok;
 
   int e, T, f_lane = 0;
+  int fl[4];
   if constexpr (ROUTE) {
-    route_expert<NT>(a, item, r_ids, r_flag, r_slots, r_misc, e, T);
-    if (MODE == 0 && blockIdx.x == 0 && tid == 0) a.dropped_out[0] = r_misc[17];
-    if (e < 0) return;
+    int dropped;
+    route_wave(a, item, e, T, fl, dropped);
+    if (MODE == 0 && blockIdx.x == 0 && tid == 0) a.dropped_out[0] = dropped;
+    if (e < 0) return;  // workgroup-uniform: every wave routes the same item
   } else {
     int blk = item;
     if (a.block_list) {
@@ -253,10 +248,20 @@ void gemv_kernel(const GemvLaunch a) {
   }
   // Flat index of the item's t-th pair (t < T).
   auto slot_of = [&](int t) -> int {
-    if constexpr (ROUTE)
-      return r_slots[t];
-    else
+    if constexpr (ROUTE) {
+      const int src = t & 63;
+      int v = __shfl(fl[0], src, 64);
+      if (T > 64) {  // uniform; ranks past 63 sit in fl[1..3]
+        const int q = t >> 6;
+        const int v1 = __shfl(fl[1], src, 64), v2 = __shfl(fl[2], src, 64);
+        const int v3 = __shfl(fl[3], src, 64);
+        v = q == 0 ? v : (q == 1 ? v1 : (q == 2 ? v2 : v3));
+      }
+      return v;
+    } else {
+      (void)fl;
       return __shfl(f_lane, t, 64);
+    }
   };
 
   const int r = lane >> 3;
@@ -469,6 +474,16 @@ size_t gemv_lds_bytes(int tc, int kdim) {
   return tc * (row_oct * sizeof(u32x4_t) + (size_t)((kdim >> 5) + 1) * sizeof(float));
 }
 
+// Fully unrolled step loops (NIT fixed at compile time) for the row lengths
+// of the benchmark shape; 0 keeps the run-time loop.  Overridable at build
+// time for tuning sweeps.
+#ifndef W4A16_W13_UNROLL
+#define W4A16_W13_UNROLL 1
+#endif
+#ifndef W4A16_W2_UNROLL
+#define W4A16_W2_UNROLL 1
+#endif
+
 template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE>
 hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   constexpr int W = kGemvWaves;
@@ -476,9 +491,9 @@ hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   if (a.n_out % rows_per_wave != 0) return hipErrorInvalidValue;
   const int chunks = a.n_out / rows_per_wave;
   const int slabs = (chunks + W - 1) / W;
-  size_t lds = gemv_lds_bytes(TC, a.kdim);
-  if (ROUTE) lds += sizeof(int) * (size_t)route_ints(a.n_tok, a.num_experts);
+  const size_t lds = gemv_lds_bytes(TC, a.kdim);
   if (lds > kMaxLds) return hipErrorInvalidValue;
+  if (ROUTE && (a.n_tok < 1 || a.n_tok > kRouteMaxTok)) return hipErrorInvalidValue;
   const int64_t grid = (int64_t)(ROUTE ? a.max_items : a.max_blocks) * slabs;
   if (grid <= 0) return hipSuccess;
   hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT, ROUTE>), dim3((unsigned)grid),
@@ -491,6 +506,8 @@ hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
 template <int MODE, int RPL, int PF, int TC, bool ROUTE>
 hipError_t launch_gemv_r(const GemvLaunch& a, hipStream_t stream) {
   const int n_it = ((a.kdim >> 5) + 7) >> 3;
+  constexpr bool unroll = MODE == 0 ? W4A16_W13_UNROLL : W4A16_W2_UNROLL;
+  if (!unroll) return launch_gemv_n<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
   switch (n_it) {
     case 4: return launch_gemv_n<MODE, RPL, PF, TC, 4, ROUTE>(a, stream);
     case 12: return launch_gemv_n<MODE, RPL, PF, TC, 12, ROUTE>(a, stream);
@@ -502,10 +519,6 @@ template <int MODE, int RPL, int PF, int TC>
 hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
   return a.ids ? launch_gemv_r<MODE, RPL, PF, TC, true>(a, stream)
                : launch_gemv_r<MODE, RPL, PF, TC, false>(a, stream);
-}
-
-size_t route_bytes(const GemvLaunch& a) {
-  return a.ids ? sizeof(int) * (size_t)route_ints(a.n_tok, a.num_experts) : 0;
 }
 
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts
@@ -523,7 +536,7 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
     tc = 1;
   else if (M < 8)
     tc = 2;
-  while (tc > 1 && gemv_lds_bytes(tc, a.kdim) + route_bytes(a) > kMaxLds) tc >>= 1;
+  while (tc > 1 && gemv_lds_bytes(tc, a.kdim) > kMaxLds) tc >>= 1;
   return tc;
 }
 
@@ -541,7 +554,7 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
 #define W4A16_W2_RPL 2
 #endif
 #ifndef W4A16_W2_PF
-#define W4A16_W2_PF 3
+#define W4A16_W2_PF 2
 #endif
 
 hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
@@ -557,8 +570,9 @@ hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
 }
 
 bool gemv_route_fits(int n_tok, int num_experts, int K, int N) {
-  const size_t route = sizeof(int) * (size_t)route_ints(n_tok, num_experts);
-  return gemv_lds_bytes(1, K) + route <= kMaxLds && gemv_lds_bytes(1, N) + route <= kMaxLds;
+  (void)num_experts;
+  return n_tok >= 1 && n_tok <= kRouteMaxTok && gemv_lds_bytes(1, K) <= kMaxLds &&
+         gemv_lds_bytes(1, N) <= kMaxLds;
 }
 
 hipError_t launch_w2_gemv(const GemvLaunch& a_in, hipStream_t stream) {

@@ -221,6 +221,22 @@ def test_duplicate_ids_in_a_row(pkg, orc, synth, dev):
            bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
 
 
+@pytest.mark.parametrize("M,topk,E,hot_slots", [(24, 10, 16, 6), (25, 10, 16, 10)])
+def test_self_routing_expert_with_many_pairs(pkg, orc, synth, dev, M, topk, E, hot_slots):
+    """Small batches route in registers; one expert holding more than 64 of
+    the (up to 256) pairs uses every rank register of the routing."""
+    shape = synth.LayerShape(E=E, topk=topk, K=256, N=256, group=32)
+    print(f"self-routing M={M} topk={topk} E={E} hot={hot_slots}", flush=True)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=11)
+    ti = ti.clone()
+    ti[:, :hot_slots] = 3  # expert 3 in hot_slots slots of every row
+    assert M * topk <= 256 and int((ti == 3).sum()) > 64
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32,
+                                  tuning=pkg.Tuning(gemv_only_max_m=M))
+    torch.cuda.synchronize()
+    _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, f"self-routing M={M}")
+
+
 def test_dtypes_and_strides(pkg, orc, synth, dev):
     shape = synth.LayerShape(E=16, topk=4, K=512, N=256, group=32)
     M = 6
