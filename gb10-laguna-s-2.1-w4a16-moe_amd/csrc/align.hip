@@ -83,16 +83,34 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   const int beg = min(n_tok, wid * per);
   const int end = min(n_tok, beg + per);
 
+  // Ids are read kBatch * 64 at a time per wave, every load issued before
+  // the first is used: one memory latency per batch, not per 64 ids.
+  constexpr int kBatch = 8;
+  auto load_batch = [&](int f0, int (&ev)[kBatch]) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int f = f0 + 64 * u + lane;
+      const int v = a.ids[min(f, max(end - 1, 0))];  // clamped, in bounds
+      ev[u] = f < end ? v : -1;
+    }
+  };
+
   // 1. per-wave histogram
   int drop = 0;
-  for (int f0 = beg; f0 < end; f0 += 64) {
-    const int f = f0 + lane;
-    if (f < end) {
-      const int e = a.ids[f];
-      if (e >= 0 && e < E)
-        atomicAdd(&cnt[wid * E + e], 1);
-      else
-        ++drop;
+  for (int f0 = beg; f0 < end; f0 += 64 * kBatch) {
+    int ev[kBatch];
+    load_batch(f0, ev);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (f0 + 64 * u >= end) break;  // uniform
+      const int f = f0 + 64 * u + lane;
+      const int e = ev[u];
+      if (f < end) {
+        if (e >= 0 && e < E)
+          atomicAdd(&cnt[wid * E + e], 1);
+        else
+          ++drop;
+      }
     }
   }
   if (drop) atomicAdd(&s_drop, drop);
@@ -170,25 +188,32 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   int ebits = 0;
   while ((1 << ebits) < E) ++ebits;
   const uint64_t lt = lanemask_lt();
-  for (int f0 = beg; f0 < end; f0 += 64) {
-    const int f = f0 + lane;
-    const int e = f < end ? a.ids[f] : -1;
-    const bool ok = f < end && e >= 0 && e < E;
-    uint64_t peers = ballot(ok);
-    for (int bit = 0; bit < ebits; ++bit) {
-      const bool set = ok && ((e >> bit) & 1);
-      const uint64_t m = ballot(set);
-      peers &= set ? m : ~m;
+  for (int fb = beg; fb < end; fb += 64 * kBatch) {
+    int ev[kBatch];
+    load_batch(fb, ev);
+    // the 64-id groups in ascending order: each advances the wave's cursors
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (fb + 64 * u >= end) break;  // uniform
+      const int f = fb + 64 * u + lane;
+      const int e = ev[u];
+      const bool ok = f < end && e >= 0 && e < E;
+      uint64_t peers = ballot(ok);
+      for (int bit = 0; bit < ebits; ++bit) {
+        const bool set = ok && ((e >> bit) & 1);
+        const uint64_t m = ballot(set);
+        peers &= set ? m : ~m;
+      }
+      int base = 0;
+      if (ok) base = cnt[wid * E + e];
+      __builtin_amdgcn_wave_barrier();
+      if (ok) {
+        const uint64_t below = peers & lt;
+        a.sorted[base + __popcll(below)] = f;
+        if (below == 0) cnt[wid * E + e] = base + __popcll(peers);
+      }
+      __builtin_amdgcn_wave_barrier();
     }
-    int base = 0;
-    if (ok) base = cnt[wid * E + e];
-    __builtin_amdgcn_wave_barrier();
-    if (ok) {
-      const uint64_t below = peers & lt;
-      a.sorted[base + __popcll(below)] = f;
-      if (below == 0) cnt[wid * E + e] = base + __popcll(peers);
-    }
-    __builtin_amdgcn_wave_barrier();
   }
 
   // 5. sentinels, expert ids, scalars

@@ -39,6 +39,7 @@ struct Tuning {
   int gemv_max_tokens;  // above it: experts with more pairs go to MFMA tiles
   int tc;               // GEMV token rows per pass (0 = launcher's choice)
   int tile_m;           // MFMA tile height
+  int upw;              // GEMV row slabs per workgroup (0 = launcher's choice)
 };
 
 struct Layout {
@@ -53,6 +54,7 @@ struct Layout {
   int64_t max_items;  // self-routed work items: one per (token, slot) pair
   int gemv_max_tokens;
   int tc;
+  int upw;
 };
 
 // An expert with more than this many (token, slot) pairs runs on MFMA tiles;
@@ -70,13 +72,13 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   return W4A16_OK;
 }
 
-Tuning default_tuning() { return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM}; }
+Tuning default_tuning() { return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0}; }
 
 // NULL selects the built-in choices; reserved fields must be zero.
 int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   *out = default_tuning();
   if (!t) return W4A16_OK;
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 3; ++i)
     if (t->reserved[i] != 0) return W4A16_ERR_INVALID_TUNING;
   if (t->gemv_only_max_m < 0) return W4A16_ERR_INVALID_TUNING;
   if (t->gemv_max_tokens < 0 || t->gemv_max_tokens >= W4A16_FUSED_BLOCK_M)
@@ -84,6 +86,9 @@ int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   const int tc = t->gemv_tokens_per_pass;
   if (tc != 0 && tc != 1 && tc != 2 && tc != 4) return W4A16_ERR_INVALID_TUNING;
   if (t->mfma_tile_m != 0 && t->mfma_tile_m != kMfmaTileM) return W4A16_ERR_INVALID_TUNING;
+  const int upw = t->gemv_units_per_wg;
+  if (upw != 0 && upw != 1 && upw != 2 && upw != 4) return W4A16_ERR_INVALID_TUNING;
+  out->upw = upw;
   out->gemv_only_max_m = t->gemv_only_max_m;
   out->gemv_max_tokens = t->gemv_max_tokens;
   out->tc = tc;
@@ -103,6 +108,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   L->mfma = M > T.gemv_only_max_m && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
   L->gemv_max_tokens = T.gemv_max_tokens;
   L->tc = T.tc;
+  L->upw = T.upw;
   const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (T.gemv_max_tokens + 1));
   L->tile_m = T.tile_m;
   L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
@@ -225,6 +231,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.max_blocks = (int32_t)L.max_gemv;
   g.num_experts = (int32_t)a.E;
   g.tc = L.tc;
+  g.upw = L.upw;
   if (L.route) {
     g.ids = a.ids;
     g.max_items = (int32_t)L.max_items;
@@ -372,6 +379,7 @@ int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts, int64
   tuning->gemv_max_tokens = T.gemv_max_tokens;
   tuning->gemv_tokens_per_pass = T.tc;
   tuning->mfma_tile_m = T.tile_m;
+  tuning->gemv_units_per_wg = T.upw;
   return W4A16_OK;
 }
 

@@ -156,6 +156,8 @@ struct GemvLaunch {
   int32_t* dropped_out;    // w13: [1] pairs with ids outside [0, E)
   int32_t tc;              // token rows per pass: 0 = chosen by the launcher,
                            // else 1, 2 or 4 (lowered while LDS does not fit)
+  int32_t upw;             // row slabs per workgroup: 0 = chosen by the
+                           // launcher, else 1, 2 or 4 (1 for run-time loops)
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);

@@ -201,22 +201,30 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
 //        0 for any other length.
 // ROUTE: the workgroup routes itself from topk_ids (no align kernel); work
 //        item i is the i-th expert with routed pairs, all of its pairs.
-template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT, bool ROUTE>
+template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT, bool ROUTE, int UPW>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(GEMV_MIN_WAVES)))
 void gemv_kernel(const GemvLaunch a) {
+  static_assert(UPW == 1 || (NIT > 0 && NIT % PF == 0), "units per workgroup need unrolled steps");
   constexpr int NR = MODE == 0 ? 2 * RPL : RPL;  // weight rows per lane
   constexpr int NT = 64 * WAVES;
   extern __shared__ u32x4_t lds[];
 
   const int rows_per_wave = 8 * RPL;
-  const int chunks = a.n_out / rows_per_wave;           // row slabs per block
-  const int slabs = (chunks + WAVES - 1) / WAVES;       // workgroups per block
-  const int item = blockIdx.x / slabs;
-  const int slab = blockIdx.x - item * slabs;
+  const int chunks = a.n_out / rows_per_wave;           // row chunks (one wave each)
+  const int slabs = (chunks + WAVES - 1) / WAVES;       // slabs of WAVES chunks
+  const int groups = (slabs + UPW - 1) / UPW;           // workgroups per item
+  const int item = blockIdx.x / groups;
+  const int slab0 = (blockIdx.x - item * groups) * UPW; // first of UPW slabs (units)
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int chunk_raw = slab * WAVES + wid;
-  const bool has_rows = chunk_raw < chunks;             // wave-uniform
-  const int chunk = has_rows ? chunk_raw : chunks - 1;  // idle waves re-read a slab
+  // Unit u covers chunk (slab0 + u) * WAVES + wid; chunks past the end are
+  // re-read from the last chunk and not stored.
+  auto unit_chunk = [&](int u, bool& valid) {
+    const int c = (slab0 + u) * WAVES + wid;
+    valid = c < chunks;  // wave-uniform
+    return valid ? c : chunks - 1;
+  };
+  bool has_rows;
+  const int chunk = unit_chunk(0, has_rows);
   const int tid = threadIdx.x;
   const int lane = __lane_id();
 
@@ -310,16 +318,24 @@ void gemv_kernel(const GemvLaunch a) {
     // the compiler wait for it there and serialise the prefetch ring.
     u32x4_t wb[PF][NR];
     uint32_t sb[PF][NR];
-    auto load_step = [&](u32x4_t (&wq)[NR], uint32_t (&sq)[NR], int it) {
+    // Step `it` of unit `u` (unit 0 = this wave's first chunk).
+    auto load_step = [&](u32x4_t (&wq)[NR], uint32_t (&sq)[NR], int u, int it) {
       // An opaque step index keeps the address math at this point: with a
       // constant index the compiler computes every step's addresses up front
       // and holds them in registers.
       asm volatile("" : "+s"(it));
       const uint32_t gi = (uint32_t)min(it * 8 + sl, G - 1);
+      uint32_t dw = 0, ds = 0;  // unit offsets from unit 0 (wave-uniform)
+      if (UPW > 1 && u > 0) {
+        bool v;
+        const uint32_t drow = (uint32_t)((unit_chunk(u, v) - chunk) * rows_per_wave);
+        dw = drow * (uint32_t)G * 16u;
+        ds = drow * (uint32_t)gpr * 2u;
+      }
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        wq[j] = *reinterpret_cast<const u32x4_t*>(wexp + (woff[j] + gi * 16u));
-        sq[j] = *reinterpret_cast<const uint16_t*>(sexp + (soff[j] + (gi >> gshift) * 2u));
+        wq[j] = *reinterpret_cast<const u32x4_t*>(wexp + (woff[j] + dw + gi * 16u));
+        sq[j] = *reinterpret_cast<const uint16_t*>(sexp + (soff[j] + ds + (gi >> gshift) * 2u));
       }
     };
     // One group step: 8 lanes per row, lane sl on group 8*it + sl; steps past
@@ -382,7 +398,10 @@ void gemv_kernel(const GemvLaunch a) {
 
 #pragma unroll
       for (int p = 0; p < PF; ++p)
-        if (NIT == 0 || p < NIT) load_step(wb[p], sb[p], min(p, n_it - 1));
+        if (NIT == 0 || p < UPW * NIT) {
+          constexpr int kN = NIT > 0 ? NIT : 1;
+          load_step(wb[p], sb[p], NIT ? p / kN : 0, NIT ? p % kN : min(p, n_it - 1));
+        }
 
       // Stage this pass's activation rows (the whole workgroup).
       __syncthreads();
@@ -394,62 +413,75 @@ void gemv_kernel(const GemvLaunch a) {
       __syncthreads();
 
       float acc[NR][NTOK];
+      auto clear = [&]() {
 #pragma unroll
-      for (int j = 0; j < NR; ++j)
+        for (int j = 0; j < NR; ++j)
 #pragma unroll
-        for (int t = 0; t < NTOK; ++t) acc[j][t] = 0.0f;
+          for (int t = 0; t < NTOK; ++t) acc[j][t] = 0.0f;
+      };
+      // Reduce each row over its 8 lanes; lane sl then owns token t0+sl.
+      auto finish = [&](int u) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j)
+#pragma unroll
+          for (int t = 0; t < NTOK; ++t) acc[j][t] = oct_sum(acc[j][t]);
+        bool valid;
+        const int cu = unit_chunk(u, valid);
+        const int nb = cu * rows_per_wave + r;
+        const int f_mine = slot_of(min(t0 + sl, T - 1));
+        if (valid && sl < tc) {
+          float v[NR];
+#pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            v[j] = acc[j][0];
+#pragma unroll
+            for (int t = 1; t < NTOK; ++t)
+              if (sl == t) v[j] = acc[j][t];
+          }
+          if (MODE == 0) {
+            uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
+#pragma unroll
+            for (int q = 0; q < RPL; ++q)
+              out[nb + 8 * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
+          } else {
+            const float wt = a.topk_w[f_mine];
+            float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
+#pragma unroll
+            for (int q = 0; q < RPL; ++q) out[nb + 8 * q] = v[q] * wt;
+          }
+        }
+      };
 
       if constexpr (NIT > 0) {
+        // UPW units back to back: the prefetch ring runs on across unit
+        // boundaries, so a unit's first steps are in flight while the
+        // previous unit finishes.
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-          compute_step(wb[it % PF], sb[it % PF], it, acc);
-          if (it + PF < NIT) load_step(wb[it % PF], sb[it % PF], it + PF);
+        for (int s = 0; s < UPW * NIT; ++s) {
+          const int u = s / NIT, it = s % NIT;
+          if (it == 0) clear();
+          compute_step(wb[s % PF], sb[s % PF], it, acc);
+          if (s + PF < UPW * NIT) load_step(wb[s % PF], sb[s % PF], (s + PF) / NIT, (s + PF) % NIT);
           // Straight-line code: keep each step's loads behind the earlier
           // steps' math, or the scheduler hoists them all and the registers
           // they hold cost occupancy.
           __builtin_amdgcn_sched_barrier(0);
+          if (it == NIT - 1) finish(u);
         }
       } else {
         // Step count known only at run time: loads stay unconditional (steps
         // past the row end re-read the last group's line, a cache hit) so
         // the same number of loads is in flight on every path.
+        clear();
         for (int it0 = 0; it0 < n_it; it0 += PF) {
 #pragma unroll
           for (int p = 0; p < PF; ++p) {
             const int it = it0 + p;
             if (it < n_it) compute_step(wb[p], sb[p], it, acc);  // wave-uniform
-            load_step(wb[p], sb[p], min(it + PF, n_it - 1));
+            load_step(wb[p], sb[p], 0, min(it + PF, n_it - 1));
           }
         }
-      }
-
-      // Reduce each row over its 8 lanes; lane sl then owns token t0+sl.
-#pragma unroll
-      for (int j = 0; j < NR; ++j)
-#pragma unroll
-        for (int t = 0; t < NTOK; ++t) acc[j][t] = oct_sum(acc[j][t]);
-
-      const int f_mine = slot_of(min(t0 + sl, T - 1));
-      if (has_rows && sl < tc) {
-        float v[NR];
-#pragma unroll
-        for (int j = 0; j < NR; ++j) {
-          v[j] = acc[j][0];
-#pragma unroll
-          for (int t = 1; t < NTOK; ++t)
-            if (sl == t) v[j] = acc[j][t];
-        }
-        if (MODE == 0) {
-          uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
-#pragma unroll
-          for (int q = 0; q < RPL; ++q)
-            out[n_base + 8 * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
-        } else {
-          const float wt = a.topk_w[f_mine];
-          float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
-#pragma unroll
-          for (int q = 0; q < RPL; ++q) out[n_base + 8 * q] = v[q] * wt;
-        }
+        finish(0);
       }
     }
   };
@@ -484,21 +516,47 @@ size_t gemv_lds_bytes(int tc, int kdim) {
 #define W4A16_W2_UNROLL 1
 #endif
 
-template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE>
+template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE, int UPW>
 hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   constexpr int W = kGemvWaves;
   const int rows_per_wave = 8 * RPL;
   if (a.n_out % rows_per_wave != 0) return hipErrorInvalidValue;
   const int chunks = a.n_out / rows_per_wave;
   const int slabs = (chunks + W - 1) / W;
+  const int groups = (slabs + UPW - 1) / UPW;
   const size_t lds = gemv_lds_bytes(TC, a.kdim);
   if (lds > kMaxLds) return hipErrorInvalidValue;
   if (ROUTE && (a.n_tok < 1 || a.n_tok > kRouteMaxTok)) return hipErrorInvalidValue;
-  const int64_t grid = (int64_t)(ROUTE ? a.max_items : a.max_blocks) * slabs;
+  const int64_t grid = (int64_t)(ROUTE ? a.max_items : a.max_blocks) * groups;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT, ROUTE>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT, ROUTE, UPW>), dim3((unsigned)grid),
                      dim3(64 * W), lds, stream, a);
   return hipGetLastError();
+}
+
+// Units (row slabs) per workgroup: a.upw, else 1.  Measured on MI355X
+// (E=256, top-10, M=4..64): more units per workgroup lose -- the w13 variant
+// drops to two waves per SIMD, and under skewed routing an expert with many
+// pairs becomes a few long workgroups (M=16 skewed: 184 vs 104 us per call).
+template <int PF, int NIT>
+int pick_upw(const GemvLaunch& a, int slabs) {
+  (void)slabs;
+  if (NIT == 0 || NIT % PF != 0) return 1;
+  return a.upw > 0 ? a.upw : 1;
+}
+
+template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE>
+hipError_t launch_gemv_u(const GemvLaunch& a, hipStream_t stream) {
+  const int chunks = a.n_out / (8 * RPL);
+  const int slabs = (chunks + kGemvWaves - 1) / kGemvWaves;
+  if constexpr (NIT > 0 && NIT % PF == 0) {
+    switch (pick_upw<PF, NIT>(a, slabs)) {
+      case 4: return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 4>(a, stream);
+      case 2: return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 2>(a, stream);
+      default: break;
+    }
+  }
+  return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 1>(a, stream);
 }
 
 // Fully unrolled step loops for the row lengths of the target layer
@@ -507,11 +565,11 @@ template <int MODE, int RPL, int PF, int TC, bool ROUTE>
 hipError_t launch_gemv_r(const GemvLaunch& a, hipStream_t stream) {
   const int n_it = ((a.kdim >> 5) + 7) >> 3;
   constexpr bool unroll = MODE == 0 ? W4A16_W13_UNROLL : W4A16_W2_UNROLL;
-  if (!unroll) return launch_gemv_n<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
+  if (!unroll) return launch_gemv_u<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
   switch (n_it) {
-    case 4: return launch_gemv_n<MODE, RPL, PF, TC, 4, ROUTE>(a, stream);
-    case 12: return launch_gemv_n<MODE, RPL, PF, TC, 12, ROUTE>(a, stream);
-    default: return launch_gemv_n<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
+    case 4: return launch_gemv_u<MODE, RPL, PF, TC, 4, ROUTE>(a, stream);
+    case 12: return launch_gemv_u<MODE, RPL, PF, TC, 12, ROUTE>(a, stream);
+    default: return launch_gemv_u<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
   }
 }
 

@@ -224,14 +224,19 @@ __global__ __launch_bounds__(256, TMB == 8 ? 1 : 2) void mfma_kernel(const MfmaL
   struct AStage {
     u32x4_t v[NA];
   };
-  auto load_a = [&](AStage& st, int step) {
+  // Octet i of a thread holds row (tid + 256 i) / 4: only the octets of the
+  // MC active token blocks (rows < 32 MC) are loaded and parked; rows of
+  // inactive blocks are never read by the MFMAs.
+  auto load_a = [&](AStage& st, int step, auto mc_c) {
+    constexpr int NAE = (decltype(mc_c)::value * 32 * 4 + 255) / 256;
     const int k = min(step, G - 1);
 #pragma unroll
-    for (int i = 0; i < NA; ++i) st.v[i] = a_src[i][k * 4];
+    for (int i = 0; i < NAE; ++i) st.v[i] = a_src[i][k * 4];
   };
-  auto store_a = [&](const AStage& st, unsigned char* Ab) {
+  auto store_a = [&](const AStage& st, unsigned char* Ab, auto mc_c) {
+    constexpr int NAE = (decltype(mc_c)::value * 32 * 4 + 255) / 256;
 #pragma unroll
-    for (int i = 0; i < NA; ++i) *reinterpret_cast<u32x4_t*>(Ab + a_lds[i]) = st.v[i];
+    for (int i = 0; i < NAE; ++i) *reinterpret_cast<u32x4_t*>(Ab + a_lds[i]) = st.v[i];
   };
   // Packed words and scale of group g for this lane's two weight rows.
   struct BRaw {
@@ -270,14 +275,24 @@ __global__ __launch_bounds__(256, TMB == 8 ? 1 : 2) void mfma_kernel(const MfmaL
         for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.0f;
 
     // Prologue: slab 0 and A(0) in LDS, A(1), A(2) and slab 1 in flight.
+    // Its loads stay in program order (scheduling barriers), the order the
+    // loop issues them in: the wait counts at the loop head merge the first
+    // entry with the back edge, and a reordered prologue would leave the
+    // loop waiting for every load in flight once per slab.
     AStage st[2];
     load_slab(0);
-    load_a(st[0], 0);
-    load_a(st[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(st[0], 0, mc_c);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(st[1], 1, mc_c);
+    __builtin_amdgcn_sched_barrier(0);
     store_slab();
-    store_a(st[0], A0);
-    load_a(st[0], 2);
+    store_a(st[0], A0, mc_c);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(st[0], 2, mc_c);
+    __builtin_amdgcn_sched_barrier(0);
     load_slab(1);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     bf16x8_t bcur[2][2], bnext[2][2];
     {
@@ -294,11 +309,13 @@ __global__ __launch_bounds__(256, TMB == 8 ? 1 : 2) void mfma_kernel(const MfmaL
         unsigned char* const Anext = A0 + ((g + 1) & 1) * kAbytes;
         // A(step+1) into the other buffer (read last in step-1, which every
         // wave has finished), then refill its registers with A(step+3).
-        store_a(st[(g + 1) & 1], Anext);
-        load_a(st[(g + 1) & 1], step + 3);
-        const bool more = step + 1 < G;  // workgroup-uniform
-        if (g == kSlab - 1 && more) {
+        store_a(st[(g + 1) & 1], Anext, mc_c);
+        load_a(st[(g + 1) & 1], step + 3, mc_c);
+        if (g == kSlab - 1) {
           // Every wave read this slab's last group in step-1: park the next.
+          // Unconditional, also after the last slab (a clamped reload whose
+          // data is never used): every path to the loop head then carries
+          // the same loads, so the waits there stay exact.
           store_slab();
           __syncthreads();
           load_slab(slab + 2);

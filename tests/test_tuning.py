@@ -30,7 +30,7 @@ def _fused_ex(lib, tuning, **kw):
 @pytest.mark.parametrize("field,value", [
     ("gemv_only_max_m", -1), ("gemv_max_tokens", -1), ("gemv_max_tokens", 16),
     ("gemv_tokens_per_pass", 3), ("gemv_tokens_per_pass", 8), ("mfma_tile_m", 64),
-    ("mfma_tile_m", 256)])
+    ("mfma_tile_m", 256), ("gemv_units_per_wg", 3), ("gemv_units_per_wg", 8)])
 def test_invalid_tuning_rejected_on_host(lib, pkg, field, value):
     t = pkg.Tuning().to_struct()
     setattr(t, field, value)
@@ -44,9 +44,9 @@ def test_invalid_tuning_rejected_on_host(lib, pkg, field, value):
 def test_default_tuning_and_workspace_sizes(pkg):
     L = pkg._lib
     d = L.default_tuning(16, 10, 256, 1024, 3072, 32)
-    assert (d.gemv_only_max_m, d.gemv_max_tokens, d.gemv_tokens_per_pass, d.mfma_tile_m) \
-        == (24, 4, 0, 128)
-    assert list(d.reserved) == [0, 0, 0, 0]
+    assert (d.gemv_only_max_m, d.gemv_max_tokens, d.gemv_tokens_per_pass, d.mfma_tile_m,
+            d.gemv_units_per_wg) == (24, 4, 0, 128, 0)
+    assert list(d.reserved) == [0, 0, 0]
     for M in (1, 16, 64, 4096):
         base = L.workspace_size(M, 10, 256, 1024, 3072, 32)
         assert L.workspace_size_ex(M, 10, 256, 1024, 3072, 32, None) == base
