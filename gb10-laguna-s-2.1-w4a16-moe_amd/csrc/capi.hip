@@ -85,7 +85,8 @@ int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
     return W4A16_ERR_INVALID_TUNING;
   const int tc = t->gemv_tokens_per_pass;
   if (tc != 0 && tc != 1 && tc != 2 && tc != 4) return W4A16_ERR_INVALID_TUNING;
-  if (t->mfma_tile_m != 0 && t->mfma_tile_m != kMfmaTileM) return W4A16_ERR_INVALID_TUNING;
+  const int tm = t->mfma_tile_m;
+  if (tm != 0 && tm != kMfmaTileM) return W4A16_ERR_INVALID_TUNING;
   const int upw = t->gemv_units_per_wg;
   if (upw != 0 && upw != 1 && upw != 2 && upw != 4) return W4A16_ERR_INVALID_TUNING;
   out->upw = upw;

@@ -61,19 +61,23 @@ def log(*a):
 def effective(M: int, N: int, K: int, t) -> tuple:
     """What a tuning does at M: the GEMV-only or the split dispatch."""
     if M <= t.gemv_only_max_m or N % 256 or K % 256:
-        return ("gemv", t.gemv_tokens_per_pass)
-    return ("split", t.gemv_max_tokens, t.gemv_tokens_per_pass)
+        return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg)
+    return ("split", t.gemv_max_tokens, t.gemv_tokens_per_pass, t.gemv_units_per_wg)
 
 
 def candidates(M: int, N: int, K: int, Tuning, always: int):
     """Every distinct dispatch choice worth timing at M, the built-in one
     first (slow candidates are pruned against it)."""
     out = [Tuning()]
-    out += [Tuning(always, 4, tc, 0) for tc in (0, 1, 2, 4) if not (tc == 1 and M > 4)]
+    for tc in (0, 1, 2, 4):
+        if tc == 1 and M > 4:
+            continue
+        out += [Tuning(always, 4, tc, 0, upw) for upw in (0, 1, 2, 4)]
     if M > 1 and N % 256 == 0 and K % 256 == 0:
         for thr in (0, 2, 4, 8, 15):
             for tc in (0, 2, 4):
                 out.append(Tuning(0, thr, tc, 0))
+        out += [Tuning(0, 4, 0, 0, upw) for upw in (1, 2, 4)]
     seen, uniq = set(), []
     for t in out:
         key = effective(M, N, K, t)

@@ -35,6 +35,7 @@ class Tuning:
     gemv_max_tokens: int = 4
     gemv_tokens_per_pass: int = 0
     mfma_tile_m: int = 0
+    gemv_units_per_wg: int = 0
 
     def to_struct(self) -> _lib.TuningStruct:
         t = _lib.TuningStruct()
@@ -42,6 +43,7 @@ class Tuning:
         t.gemv_max_tokens = int(self.gemv_max_tokens)
         t.gemv_tokens_per_pass = int(self.gemv_tokens_per_pass)
         t.mfma_tile_m = int(self.mfma_tile_m)
+        t.gemv_units_per_wg = int(self.gemv_units_per_wg)
         return t
 
     @classmethod

@@ -201,7 +201,9 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *                         the MFMA kernels, the others to the GEMV kernels;
  *   gemv_tokens_per_pass  token rows one GEMV pass reads the weights for:
  *                         0 (the library's choice), 1, 2 or 4;
- *   mfma_tile_m           MFMA tile height in slots: 0 (default) or 128.
+ *   mfma_tile_m           MFMA tile height in slots: 0 (default) or 128;
+ *   gemv_units_per_wg     64-row slabs one GEMV workgroup streams back to
+ *                         back: 0 (the library's choice), 1, 2 or 4.
  * reserved must be zero.  Every choice computes the same function; the
  * GEMV and MFMA kernels differ only in rounding (within the tolerance of
  * fused_experts).  A NULL tuning selects w4a16_moe_default_tuning's values.
@@ -211,7 +213,8 @@ typedef struct w4a16_moe_tuning {
   int32_t gemv_max_tokens;
   int32_t gemv_tokens_per_pass;
   int32_t mfma_tile_m;
-  int32_t reserved[4];
+  int32_t gemv_units_per_wg;
+  int32_t reserved[3];
 } w4a16_moe_tuning;
 
 /* The built-in tuning for a shape (what NULL selects).  No counterpart in the
