@@ -40,6 +40,7 @@ struct Tuning {
   int tc;               // GEMV token rows per pass (0 = launcher's choice)
   int tile_m;           // MFMA tile height
   int upw;              // GEMV row slabs per workgroup (0 = launcher's choice)
+  int lpr;              // GEMV lanes per weight row (0 = launcher's choice)
 };
 
 struct Layout {
@@ -55,6 +56,7 @@ struct Layout {
   int gemv_max_tokens;
   int tc;
   int upw;
+  int lpr;
 };
 
 // An expert with more than this many (token, slot) pairs runs on MFMA tiles;
@@ -72,14 +74,17 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   return W4A16_OK;
 }
 
-Tuning default_tuning() { return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0}; }
+Tuning default_tuning() { return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0}; }
 
 // NULL selects the built-in choices; reserved fields must be zero.
 int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   *out = default_tuning();
   if (!t) return W4A16_OK;
-  for (int i = 0; i < 3; ++i)
+  for (int i = 0; i < 2; ++i)
     if (t->reserved[i] != 0) return W4A16_ERR_INVALID_TUNING;
+  const int lpr = t->gemv_lanes_per_row;
+  if (lpr != 0 && lpr != 8 && lpr != 32) return W4A16_ERR_INVALID_TUNING;
+  out->lpr = lpr;
   if (t->gemv_only_max_m < 0) return W4A16_ERR_INVALID_TUNING;
   if (t->gemv_max_tokens < 0 || t->gemv_max_tokens >= W4A16_FUSED_BLOCK_M)
     return W4A16_ERR_INVALID_TUNING;
@@ -110,6 +115,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   L->gemv_max_tokens = T.gemv_max_tokens;
   L->tc = T.tc;
   L->upw = T.upw;
+  L->lpr = T.lpr;
   const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (T.gemv_max_tokens + 1));
   L->tile_m = T.tile_m;
   L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
@@ -233,6 +239,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.num_experts = (int32_t)a.E;
   g.tc = L.tc;
   g.upw = L.upw;
+  g.lpr = L.lpr;
   if (L.route) {
     g.ids = a.ids;
     g.max_items = (int32_t)L.max_items;
@@ -381,6 +388,7 @@ int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts, int64
   tuning->gemv_tokens_per_pass = T.tc;
   tuning->mfma_tile_m = T.tile_m;
   tuning->gemv_units_per_wg = T.upw;
+  tuning->gemv_lanes_per_row = T.lpr;
   return W4A16_OK;
 }
 

@@ -158,6 +158,8 @@ struct GemvLaunch {
                            // else 1, 2 or 4 (lowered while LDS does not fit)
   int32_t upw;             // row slabs per workgroup: 0 = chosen by the
                            // launcher, else 1, 2 or 4 (1 for run-time loops)
+  int32_t lpr;             // lanes per weight row: 0 = chosen by the launcher,
+                           // else 8 or 32 (32 for passes of at most 2 tokens)
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);

@@ -107,6 +107,15 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 #define GEMV_MIN_WAVES 1
 #endif
 
+// Sum over aligned groups of LPR lanes; every lane of the group gets it.
+template <int LPR>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  v = oct_sum(v);
+  if constexpr (LPR >= 16) v += dpp_f32<0x140>(v);  // row_mirror: the other 8
+  if constexpr (LPR >= 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
 // Self-routing handles at most this many (token, slot) pairs: four per lane.
 constexpr int kRouteMaxTok = 256;
 
@@ -201,15 +210,17 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
 //        0 for any other length.
 // ROUTE: the workgroup routes itself from topk_ids (no align kernel); work
 //        item i is the i-th expert with routed pairs, all of its pairs.
-template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT, bool ROUTE, int UPW>
+template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT, bool ROUTE, int UPW, int LPR>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(GEMV_MIN_WAVES)))
 void gemv_kernel(const GemvLaunch a) {
   static_assert(UPW == 1 || (NIT > 0 && NIT % PF == 0), "units per workgroup need unrolled steps");
+  static_assert(LPR == 8 || LPR == 16 || LPR == 32, "lanes per row");
   constexpr int NR = MODE == 0 ? 2 * RPL : RPL;  // weight rows per lane
   constexpr int NT = 64 * WAVES;
+  constexpr int RG = 64 / LPR;                   // row groups per wave
   extern __shared__ u32x4_t lds[];
 
-  const int rows_per_wave = 8 * RPL;
+  const int rows_per_wave = RG * RPL;
   const int chunks = a.n_out / rows_per_wave;           // row chunks (one wave each)
   const int slabs = (chunks + WAVES - 1) / WAVES;       // slabs of WAVES chunks
   const int groups = (slabs + UPW - 1) / UPW;           // workgroups per item
@@ -272,8 +283,8 @@ void gemv_kernel(const GemvLaunch a) {
     }
   };
 
-  const int r = lane >> 3;
-  const int sl = lane & 7;
+  const int r = lane / LPR;
+  const int sl = lane % LPR;
 
   const int kdim = a.kdim;
   const int G = kdim >> 5;               // 32-element groups per row
@@ -296,14 +307,14 @@ void gemv_kernel(const GemvLaunch a) {
   for (int j = 0; j < NR; ++j) {
     int row;
     if (MODE == 0)
-      row = (j < RPL) ? n_base + 8 * j : a.n_out + n_base + 8 * (j - RPL);
+      row = (j < RPL) ? n_base + RG * j : a.n_out + n_base + RG * (j - RPL);
     else
-      row = n_base + 8 * j;
+      row = n_base + RG * j;
     woff[j] = (uint32_t)row * (uint32_t)G * 16u;
     soff[j] = (uint32_t)row * (uint32_t)gpr * 2u;
   }
 
-  const int n_it = (G + 7) >> 3;
+  const int n_it = (G + LPR - 1) / LPR;
 
   // The whole item for NTOK (compile-time) tokens per pass.  Every variant
   // owns its prefetch ring: sharing one ring between variants lets the
@@ -324,7 +335,7 @@ void gemv_kernel(const GemvLaunch a) {
       // constant index the compiler computes every step's addresses up front
       // and holds them in registers.
       asm volatile("" : "+s"(it));
-      const uint32_t gi = (uint32_t)min(it * 8 + sl, G - 1);
+      const uint32_t gi = (uint32_t)min(it * LPR + sl, G - 1);
       uint32_t dw = 0, ds = 0;  // unit offsets from unit 0 (wave-uniform)
       if (UPW > 1 && u > 0) {
         bool v;
@@ -342,7 +353,7 @@ void gemv_kernel(const GemvLaunch a) {
     // the row end meet the zero activation group and add nothing.
     auto compute_step = [&](const u32x4_t (&wq)[NR], const uint32_t (&sq)[NR], int it,
                             float (&acc)[NR][NTOK]) {
-      const int gi = it * 8 + sl;
+      const int gi = it * LPR + sl;
       const int gl = gi < G ? gi : G;
       float pj[NR][NTOK];
 #pragma unroll
@@ -424,7 +435,7 @@ void gemv_kernel(const GemvLaunch a) {
 #pragma unroll
         for (int j = 0; j < NR; ++j)
 #pragma unroll
-          for (int t = 0; t < NTOK; ++t) acc[j][t] = oct_sum(acc[j][t]);
+          for (int t = 0; t < NTOK; ++t) acc[j][t] = lane_group_sum<LPR>(acc[j][t]);
         bool valid;
         const int cu = unit_chunk(u, valid);
         const int nb = cu * rows_per_wave + r;
@@ -442,12 +453,12 @@ void gemv_kernel(const GemvLaunch a) {
             uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
 #pragma unroll
             for (int q = 0; q < RPL; ++q)
-              out[nb + 8 * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
+              out[nb + RG * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
           } else {
             const float wt = a.topk_w[f_mine];
             float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
 #pragma unroll
-            for (int q = 0; q < RPL; ++q) out[nb + 8 * q] = v[q] * wt;
+            for (int q = 0; q < RPL; ++q) out[nb + RG * q] = v[q] * wt;
           }
         }
       };
@@ -516,10 +527,10 @@ size_t gemv_lds_bytes(int tc, int kdim) {
 #define W4A16_W2_UNROLL 1
 #endif
 
-template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE, int UPW>
+template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE, int UPW, int LPR>
 hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   constexpr int W = kGemvWaves;
-  const int rows_per_wave = 8 * RPL;
+  const int rows_per_wave = (64 / LPR) * RPL;
   if (a.n_out % rows_per_wave != 0) return hipErrorInvalidValue;
   const int chunks = a.n_out / rows_per_wave;
   const int slabs = (chunks + W - 1) / W;
@@ -529,7 +540,7 @@ hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   if (ROUTE && (a.n_tok < 1 || a.n_tok > kRouteMaxTok)) return hipErrorInvalidValue;
   const int64_t grid = (int64_t)(ROUTE ? a.max_items : a.max_blocks) * groups;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT, ROUTE, UPW>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gemv_kernel<MODE, RPL, PF, TC, W, NIT, ROUTE, UPW, LPR>), dim3((unsigned)grid),
                      dim3(64 * W), lds, stream, a);
   return hipGetLastError();
 }
@@ -545,38 +556,47 @@ int pick_upw(const GemvLaunch& a, int slabs) {
   return a.upw > 0 ? a.upw : 1;
 }
 
-template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE>
+template <int MODE, int RPL, int PF, int TC, int NIT, bool ROUTE, int LPR>
 hipError_t launch_gemv_u(const GemvLaunch& a, hipStream_t stream) {
-  const int chunks = a.n_out / (8 * RPL);
+  const int chunks = a.n_out / ((64 / LPR) * RPL);
   const int slabs = (chunks + kGemvWaves - 1) / kGemvWaves;
-  if constexpr (NIT > 0 && NIT % PF == 0) {
+  if constexpr (LPR == 8 && NIT > 0 && NIT % PF == 0) {
     switch (pick_upw<PF, NIT>(a, slabs)) {
-      case 4: return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 4>(a, stream);
-      case 2: return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 2>(a, stream);
+      case 4: return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 4, LPR>(a, stream);
+      case 2: return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 2, LPR>(a, stream);
       default: break;
     }
   }
-  return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 1>(a, stream);
+  return launch_gemv_n<MODE, RPL, PF, TC, NIT, ROUTE, 1, LPR>(a, stream);
 }
 
 // Fully unrolled step loops for the row lengths of the target layer
 // (K = 3072: 12 steps; N = 1024: 4 steps); any other length runs the loop.
-template <int MODE, int RPL, int PF, int TC, bool ROUTE>
+template <int MODE, int RPL, int PF, int TC, bool ROUTE, int LPR>
 hipError_t launch_gemv_r(const GemvLaunch& a, hipStream_t stream) {
-  const int n_it = ((a.kdim >> 5) + 7) >> 3;
+  const int n_it = ((a.kdim >> 5) + LPR - 1) / LPR;
   constexpr bool unroll = MODE == 0 ? W4A16_W13_UNROLL : W4A16_W2_UNROLL;
-  if (!unroll) return launch_gemv_u<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
-  switch (n_it) {
-    case 4: return launch_gemv_u<MODE, RPL, PF, TC, 4, ROUTE>(a, stream);
-    case 12: return launch_gemv_u<MODE, RPL, PF, TC, 12, ROUTE>(a, stream);
-    default: return launch_gemv_u<MODE, RPL, PF, TC, 0, ROUTE>(a, stream);
+  if (!unroll) return launch_gemv_u<MODE, RPL, PF, TC, 0, ROUTE, LPR>(a, stream);
+  if constexpr (LPR == 8) {
+    switch (n_it) {
+      case 4: return launch_gemv_u<MODE, RPL, PF, TC, 4, ROUTE, LPR>(a, stream);
+      case 12: return launch_gemv_u<MODE, RPL, PF, TC, 12, ROUTE, LPR>(a, stream);
+      default: break;
+    }
+  } else if constexpr (LPR == 32) {
+    switch (n_it) {
+      case 1: return launch_gemv_u<MODE, RPL, PF, TC, 1, ROUTE, LPR>(a, stream);
+      case 3: return launch_gemv_u<MODE, RPL, PF, TC, 3, ROUTE, LPR>(a, stream);
+      default: break;
+    }
   }
+  return launch_gemv_u<MODE, RPL, PF, TC, 0, ROUTE, LPR>(a, stream);
 }
 
-template <int MODE, int RPL, int PF, int TC>
+template <int MODE, int RPL, int PF, int TC, int LPR = 8>
 hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
-  return a.ids ? launch_gemv_r<MODE, RPL, PF, TC, true>(a, stream)
-               : launch_gemv_r<MODE, RPL, PF, TC, false>(a, stream);
+  return a.ids ? launch_gemv_r<MODE, RPL, PF, TC, true, LPR>(a, stream)
+               : launch_gemv_r<MODE, RPL, PF, TC, false, LPR>(a, stream);
 }
 
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts
@@ -615,16 +635,36 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
 #define W4A16_W2_PF 2
 #endif
 
+// Lanes per weight row: a.lpr, or by default 32 for the w13 launch of
+// one-token passes (M = 1), which is short of loads in flight -- 32 lanes per
+// row put a whole K = 3072 row's loads in flight at once (M=1: 12.0 -> 11.0
+// us) -- and 8 otherwise (whole 128-byte lines per step, the fewest lanes
+// per byte; w2's short rows would become many tiny workgroups: 6.8 -> 8.3
+// us).  32 exists for passes of 1 or 2 tokens.
+int pick_lpr(const GemvLaunch& a, int tc, int mode) {
+  if (tc > 2) return 8;
+  if (a.lpr > 0) return a.lpr == 32 ? 32 : 8;
+  return (mode == 0 && tc == 1) ? 32 : 8;
+}
+
+template <int MODE, int R, int P>
+hipError_t launch_gemv_tc(const GemvLaunch& a, hipStream_t stream) {
+  const int tc = pick_tc(a, a.num_experts);
+  const bool wide = pick_lpr(a, tc, MODE) == 32;
+  switch (tc) {
+    case 1: return wide ? launch_gemv_t<MODE, R, P, 1, 32>(a, stream)
+                        : launch_gemv_t<MODE, R, P, 1>(a, stream);
+    case 2: return wide ? launch_gemv_t<MODE, R, P, 2, 32>(a, stream)
+                        : launch_gemv_t<MODE, R, P, 2>(a, stream);
+    default: return launch_gemv_t<MODE, R, P, 4>(a, stream);
+  }
+}
+
 hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
   GemvLaunch a = a_in;
   a.nib_mask = 0x000F000Fu;
   a.nib_magic = 0x43004300u;  // bf16 (128, 128)
-  constexpr int R = W4A16_W13_RPL, P = W4A16_W13_PF;
-  switch (pick_tc(a, a.num_experts)) {
-    case 1: return launch_gemv_t<0, R, P, 1>(a, stream);
-    case 2: return launch_gemv_t<0, R, P, 2>(a, stream);
-    default: return launch_gemv_t<0, R, P, 4>(a, stream);
-  }
+  return launch_gemv_tc<0, W4A16_W13_RPL, W4A16_W13_PF>(a, stream);
 }
 
 bool gemv_route_fits(int n_tok, int num_experts, int K, int N) {
@@ -637,12 +677,7 @@ hipError_t launch_w2_gemv(const GemvLaunch& a_in, hipStream_t stream) {
   GemvLaunch a = a_in;
   a.nib_mask = 0x000F000Fu;
   a.nib_magic = 0x43004300u;
-  constexpr int R = W4A16_W2_RPL, P = W4A16_W2_PF;
-  switch (pick_tc(a, a.num_experts)) {
-    case 1: return launch_gemv_t<1, R, P, 1>(a, stream);
-    case 2: return launch_gemv_t<1, R, P, 2>(a, stream);
-    default: return launch_gemv_t<1, R, P, 4>(a, stream);
-  }
+  return launch_gemv_tc<1, W4A16_W2_RPL, W4A16_W2_PF>(a, stream);
 }
 
 }  // namespace w4a16

@@ -61,8 +61,9 @@ def log(*a):
 def effective(M: int, N: int, K: int, t) -> tuple:
     """What a tuning does at M: the GEMV-only or the split dispatch."""
     if M <= t.gemv_only_max_m or N % 256 or K % 256:
-        return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg)
-    return ("split", t.gemv_max_tokens, t.gemv_tokens_per_pass, t.gemv_units_per_wg)
+        return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg, t.gemv_lanes_per_row)
+    return ("split", t.gemv_max_tokens, t.gemv_tokens_per_pass, t.gemv_units_per_wg,
+            t.gemv_lanes_per_row)
 
 
 def candidates(M: int, N: int, K: int, Tuning, always: int):
@@ -73,6 +74,8 @@ def candidates(M: int, N: int, K: int, Tuning, always: int):
         if tc == 1 and M > 4:
             continue
         out += [Tuning(always, 4, tc, 0, upw) for upw in (0, 1, 2, 4)]
+        if tc in (0, 1, 2):
+            out += [Tuning(always, 4, tc, 0, 0, lpr) for lpr in (8, 32)]
     if M > 1 and N % 256 == 0 and K % 256 == 0:
         for thr in (0, 2, 4, 8, 15):
             for tc in (0, 2, 4):

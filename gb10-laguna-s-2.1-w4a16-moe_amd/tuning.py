@@ -36,6 +36,7 @@ class Tuning:
     gemv_tokens_per_pass: int = 0
     mfma_tile_m: int = 0
     gemv_units_per_wg: int = 0
+    gemv_lanes_per_row: int = 0
 
     def to_struct(self) -> _lib.TuningStruct:
         t = _lib.TuningStruct()
@@ -44,6 +45,7 @@ class Tuning:
         t.gemv_tokens_per_pass = int(self.gemv_tokens_per_pass)
         t.mfma_tile_m = int(self.mfma_tile_m)
         t.gemv_units_per_wg = int(self.gemv_units_per_wg)
+        t.gemv_lanes_per_row = int(self.gemv_lanes_per_row)
         return t
 
     @classmethod

@@ -203,7 +203,10 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *                         0 (the library's choice), 1, 2 or 4;
  *   mfma_tile_m           MFMA tile height in slots: 0 (default) or 128;
  *   gemv_units_per_wg     64-row slabs one GEMV workgroup streams back to
- *                         back: 0 (the library's choice), 1, 2 or 4.
+ *                         back: 0 (the library's choice), 1, 2 or 4;
+ *   gemv_lanes_per_row    lanes sharing one GEMV weight row: 0 (the
+ *                         library's choice), 8 or 32 (32 applies to passes
+ *                         of at most 2 token rows).
  * reserved must be zero.  Every choice computes the same function; the
  * GEMV and MFMA kernels differ only in rounding (within the tolerance of
  * fused_experts).  A NULL tuning selects w4a16_moe_default_tuning's values.
@@ -214,7 +217,8 @@ typedef struct w4a16_moe_tuning {
   int32_t gemv_tokens_per_pass;
   int32_t mfma_tile_m;
   int32_t gemv_units_per_wg;
-  int32_t reserved[3];
+  int32_t gemv_lanes_per_row;
+  int32_t reserved[2];
 } w4a16_moe_tuning;
 
 /* The built-in tuning for a shape (what NULL selects).  No counterpart in the
