@@ -53,6 +53,7 @@ struct Layout {
   int64_t max_tiles;  // bound of the MFMA tile list
   int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
   int64_t max_items;  // self-routed work items: one per (token, slot) pair
+  bool token;         // one token: w2 and the combine in one launch
   int gemv_max_tokens;
   int tc;
   int upw;
@@ -126,6 +127,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   L->route = !L->mfma && M >= 1 && M <= T.gemv_only_max_m &&
              gemv_route_fits((int)n_tok, (int)E, (int)K, (int)N);
   L->max_items = L->route ? (int64_t)n_tok : 0;
+  L->token = L->route && M == 1 && w2_token_fits((int)topk, (int)K, (int)N);
   size_t cur = 0;
   auto put = [&](int field, size_t bytes) {
     L->off[field] = cur;
@@ -286,7 +288,11 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.out = partial;
   g.n_out = (int32_t)a.K;
   g.kdim = (int32_t)a.N;
-  if (want(2) && launch_w2_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(2)) {
+    const hipError_t st = L.token ? launch_w2_token(g, static_cast<uint16_t*>(a.out), stream)
+                                  : launch_w2_gemv(g, stream);
+    if (st != hipSuccess) return W4A16_ERR_HIP;
+  }
   if (L.mfma && want(2)) {
     m.act = inter;
     m.ld_act = a.N;
@@ -309,7 +315,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   c.topk = (int32_t)a.topk;
   c.K = (int32_t)a.K;
   c.num_experts = (int32_t)a.E;
-  if (want(3) && launch_combine(c, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(3) && !L.token && launch_combine(c, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (ev && hipEventRecord(ev[4], stream) != hipSuccess) return W4A16_ERR_HIP;
   return W4A16_OK;
 }

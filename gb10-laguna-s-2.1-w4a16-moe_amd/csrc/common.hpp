@@ -163,6 +163,10 @@ struct GemvLaunch {
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);
+// One-token calls: w2 and the top-k combine in one launch, writing the bf16
+// output row `out` (the activations are the token's topk intermediate rows).
+bool w2_token_fits(int topk, int K, int N);
+hipError_t launch_w2_token(const GemvLaunch& a, uint16_t* out, hipStream_t stream);
 // Self-routing: whether the routing tables plus one staged row fit in LDS.
 bool gemv_route_fits(int n_tok, int num_experts, int K, int N);
 

@@ -72,12 +72,11 @@ __device__ __forceinline__ float word_dot(uint32_t w, const u32x4_t& x, float ac
 }
 
 // Stage one bf16 activation row of kdim values into LDS, permuted into the
-// pair order word_dot expects, plus the per-group offset correction C.  All
-// NT threads of the workgroup take part.
+// pair order word_dot expects, plus the per-group offset correction C.  NT
+// threads take part, thread `tid` (NT a multiple of 64, tid in [0, NT)).
 template <int NT>
 __device__ __forceinline__ void stage_row(const uint16_t* __restrict__ src, int kdim,
-                                          u32x4_t* xp, float* xc) {
-  const int tid = threadIdx.x;
+                                          u32x4_t* xp, float* xc, int tid) {
   const int n_oct = kdim >> 3;
   const u32x4_t* s4 = reinterpret_cast<const u32x4_t*>(src);
   // octets n_oct .. n_oct+3 form the zero group
@@ -419,7 +418,8 @@ void gemv_kernel(const GemvLaunch a) {
       for (int t = 0; t < tc; ++t) {
         const int f = slot_of(t0 + t);
         const int64_t arow = MODE == 0 ? f / a.topk : f;
-        stage_row<NT>(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * xc_pitch);
+        stage_row<NT>(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * xc_pitch,
+                      tid);
       }
       __syncthreads();
 
@@ -503,6 +503,110 @@ void gemv_kernel(const GemvLaunch a) {
   else if (TC >= 3 && tcap == 3) body(std::integral_constant<int, (TC >= 3 ? 3 : 1)>{});
   else if (TC >= 2 && tcap == 2) body(std::integral_constant<int, (TC >= 2 ? 2 : 1)>{});
   else body(std::integral_constant<int, 1>{});
+}
+
+// The w2 GEMV and the top-k combine of a one-token call in one launch.
+//
+// A workgroup has one wave per slot (topk <= 16) and owns 8 output rows.
+// Wave t computes slot t's 8 rows exactly as gemv_kernel<1, ...> does (8
+// lanes per row on groups 8*it + lane%8, the same dot2 chain per word and
+// fma per group, the same 8-lane sum), multiplies by the routing weight and
+// parks the value in LDS.  The workgroup then adds the slots in order from
+// 0.0, skipping ids outside [0, E), as combine_kernel does.  The result is
+// therefore bit-identical to gemv_kernel + combine_kernel, with one launch,
+// no partial rows in memory, and every wave's weight loads in flight at once.
+template <int NIT>
+__global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint16_t* out) {
+  extern __shared__ u32x4_t lds[];
+  const int topk = a.topk;
+  const int t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's slot
+  const int lane = __lane_id();
+  const int kdim = a.kdim;
+  const int G = kdim >> 5;
+  const int gpr = kdim / a.group;
+  const int gshift = a.group == 32 ? 0 : (a.group == 64 ? 1 : 2);
+  const int row_oct = staged_row_octets(kdim);
+  u32x4_t* xp = lds + t * row_oct;
+  float* xc = reinterpret_cast<float*>(lds + topk * row_oct) + t * (G + 1);
+  float* red = reinterpret_cast<float*>(lds + topk * row_oct) + topk * (G + 1);  // [topk][8]
+
+  const int E = a.num_experts;
+  const int e_raw = a.ids[t];
+  const bool valid = e_raw >= 0 && e_raw < E;  // wave-uniform
+  const int e = valid ? e_raw : 0;
+  stage_row<64>(a.act + (int64_t)t * a.ld_act, kdim, xp, xc, lane);
+
+  const int r = lane >> 3, sl = lane & 7;
+  const int row = blockIdx.x * 8 + r;
+  const char* wrow = reinterpret_cast<const char*>(a.w) + ((int64_t)e * a.n_out + row) * G * 16;
+  const char* srow = reinterpret_cast<const char*>(a.s) + ((int64_t)e * a.n_out + row) * gpr * 2;
+  const uint32_t mask = a.nib_mask;
+  uint32_t magic;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.nib_magic));
+  const int n_it = NIT > 0 ? NIT : (G + 7) >> 3;
+  constexpr int kMaxIt = NIT > 0 ? NIT : 1;
+
+  // All loads first (NIT of them), then the staged row is ready.
+  u32x4_t wq[kMaxIt];
+  uint32_t sq[kMaxIt];
+  if constexpr (NIT > 0) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int gi = min(it * 8 + sl, G - 1);
+      wq[it] = *reinterpret_cast<const u32x4_t*>(wrow + gi * 16);
+      sq[it] = *reinterpret_cast<const uint16_t*>(srow + (gi >> gshift) * 2);
+    }
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  auto step = [&](const u32x4_t& w4, uint32_t sbits, int it) {
+    const int gi = it * 8 + sl;
+    const int gl = gi < G ? gi : G;
+    float pj = xc[gl];  // -C
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const u32x4_t x = xp[lds_octet(gl * 4 + w)];
+      const uint32_t wv = w4[w];
+      const uint32_t d0 = (wv & mask) | magic;
+      const uint32_t d1 = ((wv >> 4) & mask) | magic;
+      const uint32_t d2 = ((wv >> 8) & mask) | magic;
+      const uint32_t d3 = ((wv >> 12) & mask) | magic;
+      float q = dot2(d0, x[0], pj);
+      q = dot2(d1, x[1], q);
+      q = dot2(d2, x[2], q);
+      pj = dot2(d3, x[3], q);
+    }
+    acc = fmaf(bf16_to_f32(sbits), pj, acc);
+  };
+  if constexpr (NIT > 0) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) step(wq[it], sq[it], it);
+  } else {
+    for (int it = 0; it < n_it; ++it) {
+      const int gi = min(it * 8 + sl, G - 1);
+      const u32x4_t w4 = *reinterpret_cast<const u32x4_t*>(wrow + gi * 16);
+      const uint32_t sb = *reinterpret_cast<const uint16_t*>(srow + (gi >> gshift) * 2);
+      step(w4, sb, it);
+    }
+  }
+  acc = oct_sum(acc);
+  if (sl == 0) red[t * 8 + r] = acc * a.topk_w[t];
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    float sum = 0.0f;
+    for (int s = 0; s < topk; ++s) {
+      const int es = a.ids[s];
+      if (es >= 0 && es < E) sum += red[s * 8 + threadIdx.x];
+    }
+    out[blockIdx.x * 8 + threadIdx.x] = (uint16_t)f32_to_bf16(sum);
+  }
+}
+
+size_t w2_token_lds_bytes(int topk, int kdim) {
+  return (size_t)topk * (staged_row_octets(kdim) * sizeof(u32x4_t) +
+                         (size_t)((kdim >> 5) + 1) * sizeof(float)) +
+         (size_t)topk * 8 * sizeof(float);
 }
 
 // The staged rows must fit the 64 KB of LDS a workgroup may use.
@@ -671,6 +775,25 @@ bool gemv_route_fits(int n_tok, int num_experts, int K, int N) {
   (void)num_experts;
   return n_tok >= 1 && n_tok <= kRouteMaxTok && gemv_lds_bytes(1, K) <= kMaxLds &&
          gemv_lds_bytes(1, N) <= kMaxLds;
+}
+
+bool w2_token_fits(int topk, int K, int N) {
+  return topk >= 1 && topk <= 16 && K % 8 == 0 && w2_token_lds_bytes(topk, N) <= kMaxLds;
+}
+
+hipError_t launch_w2_token(const GemvLaunch& a_in, uint16_t* out, hipStream_t stream) {
+  GemvLaunch a = a_in;
+  a.nib_mask = 0x000F000Fu;
+  a.nib_magic = 0x43004300u;
+  if (!w2_token_fits(a.topk, a.n_out, a.kdim)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(a.n_out / 8)), block(64 * a.topk);
+  const size_t lds = w2_token_lds_bytes(a.topk, a.kdim);
+  const int n_it = ((a.kdim >> 5) + 7) >> 3;
+  if (n_it == 4)
+    hipLaunchKernelGGL(w2_token_kernel<4>, grid, block, lds, stream, a, out);
+  else
+    hipLaunchKernelGGL(w2_token_kernel<0>, grid, block, lds, stream, a, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_w2_gemv(const GemvLaunch& a_in, hipStream_t stream) {

@@ -237,6 +237,31 @@ def test_self_routing_expert_with_many_pairs(pkg, orc, synth, dev, M, topk, E, h
     _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, f"self-routing M={M}")
 
 
+@pytest.mark.parametrize("E,topk,K,N,group", [(16, 10, 512, 256, 32), (8, 4, 1024, 512, 64),
+                                              (32, 16, 256, 1024, 32), (256, 10, 3072, 1024, 32),
+                                              (8, 1, 256, 256, 128)])
+@pytest.mark.parametrize("drop", [False, True])
+def test_one_token_w2_with_combine_bit_identical(pkg, orc, synth, dev, E, topk, K, N, group,
+                                                 drop):
+    """M = 1 runs w2 and the top-k sum in one launch; it must equal the
+    separate GEMV + combine kernels bit for bit (the split dispatch, forced
+    by the tuning, takes that route)."""
+    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=group)
+    print(f"one-token E={E} topk={topk} K={K} N={N} G={group} drop={drop}", flush=True)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, 1, dev, seed=E + topk)
+    if drop:
+        ti = ti.clone()
+        ti[0, -1] = E        # out of range: skipped
+        if topk > 2:
+            ti[0, 0] = ti[0, 1]  # the same expert twice
+    fused = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group)
+    split = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group,
+                                    tuning=pkg.Tuning(gemv_only_max_m=0))
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
+    _check(orc, fused, x, w13, w2, s13, s2, tw, ti, group, "one-token")
+
+
 def test_dtypes_and_strides(pkg, orc, synth, dev):
     shape = synth.LayerShape(E=16, topk=4, K=512, N=256, group=32)
     M = 6
