@@ -41,6 +41,7 @@ struct Tuning {
   int tile_m;           // MFMA tile height
   int upw;              // GEMV row slabs per workgroup (0 = launcher's choice)
   int lpr;              // GEMV lanes per weight row (0 = launcher's choice)
+  int w2_fused_max_m;   // M at or below this: w2 and the top-k sum as one kernel
 };
 
 struct Layout {
@@ -64,6 +65,11 @@ struct Layout {
 // the others stay on the GEMV kernels.  Must stay below the sort block (16).
 constexpr int kGemvMaxTokens = W4A16_GEMV_MAX_TOKENS;
 constexpr int kGemvOnlyMaxM = W4A16_GEMV_ONLY_MAX_M;
+// Self-routed calls up to this many tokens run w2 and the top-k sum as one
+// kernel.  Measured on MI355X (E=256, top-10): M=2 28.6 vs 30.9 us, M=4
+// 48.1 vs 49.1 us (skewed routing 40.9 vs 44.7); at M=8 the experts shared
+// by tokens, read once per token, cancel the saved launch.
+constexpr int kW2FusedMaxM = 4;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -75,14 +81,17 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   return W4A16_OK;
 }
 
-Tuning default_tuning() { return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0}; }
+Tuning default_tuning() {
+  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0, kW2FusedMaxM};
+}
 
 // NULL selects the built-in choices; reserved fields must be zero.
 int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   *out = default_tuning();
   if (!t) return W4A16_OK;
-  for (int i = 0; i < 2; ++i)
-    if (t->reserved[i] != 0) return W4A16_ERR_INVALID_TUNING;
+  if (t->reserved[0] != 0) return W4A16_ERR_INVALID_TUNING;
+  if (t->w2_fused_max_m < 0) return W4A16_ERR_INVALID_TUNING;
+  if (t->w2_fused_max_m > 0) out->w2_fused_max_m = t->w2_fused_max_m;
   const int lpr = t->gemv_lanes_per_row;
   if (lpr != 0 && lpr != 8 && lpr != 32) return W4A16_ERR_INVALID_TUNING;
   out->lpr = lpr;
@@ -127,7 +136,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   L->route = !L->mfma && M >= 1 && M <= T.gemv_only_max_m &&
              gemv_route_fits((int)n_tok, (int)E, (int)K, (int)N);
   L->max_items = L->route ? (int64_t)n_tok : 0;
-  L->token = L->route && M == 1 && w2_token_fits((int)topk, (int)K, (int)N);
+  L->token = L->route && M <= T.w2_fused_max_m && w2_token_fits((int)topk, (int)K, (int)N);
   size_t cur = 0;
   auto put = [&](int field, size_t bytes) {
     L->off[field] = cur;
@@ -289,8 +298,9 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.n_out = (int32_t)a.K;
   g.kdim = (int32_t)a.N;
   if (want(2)) {
-    const hipError_t st = L.token ? launch_w2_token(g, static_cast<uint16_t*>(a.out), stream)
-                                  : launch_w2_gemv(g, stream);
+    const hipError_t st = L.token
+                              ? launch_w2_token(g, static_cast<uint16_t*>(a.out), a.ld_out, stream)
+                              : launch_w2_gemv(g, stream);
     if (st != hipSuccess) return W4A16_ERR_HIP;
   }
   if (L.mfma && want(2)) {
@@ -395,6 +405,7 @@ int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts, int64
   tuning->mfma_tile_m = T.tile_m;
   tuning->gemv_units_per_wg = T.upw;
   tuning->gemv_lanes_per_row = T.lpr;
+  tuning->w2_fused_max_m = T.w2_fused_max_m;
   return W4A16_OK;
 }
 

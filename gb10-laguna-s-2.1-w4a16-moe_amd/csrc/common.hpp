@@ -163,10 +163,11 @@ struct GemvLaunch {
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);
-// One-token calls: w2 and the top-k combine in one launch, writing the bf16
-// output row `out` (the activations are the token's topk intermediate rows).
+// Few-token calls: w2 and the top-k combine in one launch, writing the bf16
+// output rows `out` (row stride ld_out) of the n_tok / topk tokens.
 bool w2_token_fits(int topk, int K, int N);
-hipError_t launch_w2_token(const GemvLaunch& a, uint16_t* out, hipStream_t stream);
+hipError_t launch_w2_token(const GemvLaunch& a, uint16_t* out, int64_t ld_out,
+                           hipStream_t stream);
 // Self-routing: whether the routing tables plus one staged row fit in LDS.
 bool gemv_route_fits(int n_tok, int num_experts, int K, int N);
 

@@ -505,9 +505,11 @@ void gemv_kernel(const GemvLaunch a) {
   else body(std::integral_constant<int, 1>{});
 }
 
-// The w2 GEMV and the top-k combine of a one-token call in one launch.
+// The w2 GEMV and the top-k combine of a few-token call in one launch.
 //
-// A workgroup has one wave per slot (topk <= 16) and owns 8 output rows.
+// A workgroup has one wave per slot (topk <= 16) and owns 8 output rows of
+// one token (blockIdx.y); an expert routed from several tokens is read once
+// per token.
 // Wave t computes slot t's 8 rows exactly as gemv_kernel<1, ...> does (8
 // lanes per row on groups 8*it + lane%8, the same dot2 chain per word and
 // fma per group, the same 8-lane sum), multiplies by the routing weight and
@@ -516,10 +518,13 @@ void gemv_kernel(const GemvLaunch a) {
 // therefore bit-identical to gemv_kernel + combine_kernel, with one launch,
 // no partial rows in memory, and every wave's weight loads in flight at once.
 template <int NIT>
-__global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint16_t* out) {
+__global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint16_t* out,
+                                                       int64_t ld_out) {
   extern __shared__ u32x4_t lds[];
   const int topk = a.topk;
   const int t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's slot
+  const int m = blockIdx.y;                                          // token
+  const int f = m * topk + t;                                        // flat slot
   const int lane = __lane_id();
   const int kdim = a.kdim;
   const int G = kdim >> 5;
@@ -531,10 +536,10 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
   float* red = reinterpret_cast<float*>(lds + topk * row_oct) + topk * (G + 1);  // [topk][8]
 
   const int E = a.num_experts;
-  const int e_raw = a.ids[t];
+  const int e_raw = a.ids[f];
   const bool valid = e_raw >= 0 && e_raw < E;  // wave-uniform
   const int e = valid ? e_raw : 0;
-  stage_row<64>(a.act + (int64_t)t * a.ld_act, kdim, xp, xc, lane);
+  stage_row<64>(a.act + (int64_t)f * a.ld_act, kdim, xp, xc, lane);
 
   const int r = lane >> 3, sl = lane & 7;
   const int row = blockIdx.x * 8 + r;
@@ -591,15 +596,15 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
     }
   }
   acc = oct_sum(acc);
-  if (sl == 0) red[t * 8 + r] = acc * a.topk_w[t];
+  if (sl == 0) red[t * 8 + r] = acc * a.topk_w[f];
   __syncthreads();
   if (threadIdx.x < 8) {
     float sum = 0.0f;
     for (int s = 0; s < topk; ++s) {
-      const int es = a.ids[s];
+      const int es = a.ids[m * topk + s];
       if (es >= 0 && es < E) sum += red[s * 8 + threadIdx.x];
     }
-    out[blockIdx.x * 8 + threadIdx.x] = (uint16_t)f32_to_bf16(sum);
+    out[(int64_t)m * ld_out + blockIdx.x * 8 + threadIdx.x] = (uint16_t)f32_to_bf16(sum);
   }
 }
 
@@ -781,18 +786,20 @@ bool w2_token_fits(int topk, int K, int N) {
   return topk >= 1 && topk <= 16 && K % 8 == 0 && w2_token_lds_bytes(topk, N) <= kMaxLds;
 }
 
-hipError_t launch_w2_token(const GemvLaunch& a_in, uint16_t* out, hipStream_t stream) {
+hipError_t launch_w2_token(const GemvLaunch& a_in, uint16_t* out, int64_t ld_out,
+                           hipStream_t stream) {
   GemvLaunch a = a_in;
   a.nib_mask = 0x000F000Fu;
   a.nib_magic = 0x43004300u;
   if (!w2_token_fits(a.topk, a.n_out, a.kdim)) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(a.n_out / 8)), block(64 * a.topk);
+  const int M = a.n_tok / a.topk;
+  const dim3 grid((unsigned)(a.n_out / 8), (unsigned)M), block(64 * a.topk);
   const size_t lds = w2_token_lds_bytes(a.topk, a.kdim);
   const int n_it = ((a.kdim >> 5) + 7) >> 3;
   if (n_it == 4)
-    hipLaunchKernelGGL(w2_token_kernel<4>, grid, block, lds, stream, a, out);
+    hipLaunchKernelGGL(w2_token_kernel<4>, grid, block, lds, stream, a, out, ld_out);
   else
-    hipLaunchKernelGGL(w2_token_kernel<0>, grid, block, lds, stream, a, out);
+    hipLaunchKernelGGL(w2_token_kernel<0>, grid, block, lds, stream, a, out, ld_out);
   return hipGetLastError();
 }
 

@@ -61,7 +61,9 @@ def log(*a):
 def effective(M: int, N: int, K: int, t) -> tuple:
     """What a tuning does at M: the GEMV-only or the split dispatch."""
     if M <= t.gemv_only_max_m or N % 256 or K % 256:
-        return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg, t.gemv_lanes_per_row)
+        fused = M <= (t.w2_fused_max_m or 4)
+        return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg, t.gemv_lanes_per_row,
+                fused)
     return ("split", t.gemv_max_tokens, t.gemv_tokens_per_pass, t.gemv_units_per_wg,
             t.gemv_lanes_per_row)
 
@@ -76,6 +78,8 @@ def candidates(M: int, N: int, K: int, Tuning, always: int):
         out += [Tuning(always, 4, tc, 0, upw) for upw in (0, 1, 2, 4)]
         if tc in (0, 1, 2):
             out += [Tuning(always, 4, tc, 0, 0, lpr) for lpr in (8, 32)]
+    if 1 < M <= 16:  # w2 with the top-k sum as one kernel
+        out += [Tuning(always, 4, tc, 0, 0, 0, M) for tc in (0, 2, 4)]
     if M > 1 and N % 256 == 0 and K % 256 == 0:
         for thr in (0, 2, 4, 8, 15):
             for tc in (0, 2, 4):

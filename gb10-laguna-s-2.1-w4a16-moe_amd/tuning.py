@@ -37,6 +37,7 @@ class Tuning:
     mfma_tile_m: int = 0
     gemv_units_per_wg: int = 0
     gemv_lanes_per_row: int = 0
+    w2_fused_max_m: int = 0
 
     def to_struct(self) -> _lib.TuningStruct:
         t = _lib.TuningStruct()
@@ -46,6 +47,7 @@ class Tuning:
         t.mfma_tile_m = int(self.mfma_tile_m)
         t.gemv_units_per_wg = int(self.gemv_units_per_wg)
         t.gemv_lanes_per_row = int(self.gemv_lanes_per_row)
+        t.w2_fused_max_m = int(self.w2_fused_max_m)
         return t
 
     @classmethod

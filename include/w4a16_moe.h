@@ -66,7 +66,7 @@ extern "C" {
 #define W4A16_WS_NFIELDS      8
 /* Calls with M <= W4A16_GEMV_ONLY_MAX_M skip the align kernel: the GEMV
  * kernels route themselves from topk_ids.  Those calls write only the
- * header's dropped count [1], INTER and PARTIAL (not PARTIAL when M = 1: w2
+ * header's dropped count [1], INTER and PARTIAL (not PARTIAL when M <= 4: w2
  * and the top-k sum then run as one kernel); the other fields keep whatever
  * they held. */
 
@@ -207,7 +207,11 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *                         back: 0 (the library's choice), 1, 2 or 4;
  *   gemv_lanes_per_row    lanes sharing one GEMV weight row: 0 (the
  *                         library's choice), 8 or 32 (32 applies to passes
- *                         of at most 2 token rows).
+ *                         of at most 2 token rows);
+ *   w2_fused_max_m        self-routed calls with M at or below this run w2
+ *                         and the top-k sum as one kernel (an expert shared
+ *                         by several tokens is then read once per token):
+ *                         0 (the library's choice: 4) or a token count.
  * reserved must be zero.  Every choice computes the same function; the
  * GEMV and MFMA kernels differ only in rounding (within the tolerance of
  * fused_experts).  A NULL tuning selects w4a16_moe_default_tuning's values.
@@ -219,7 +223,8 @@ typedef struct w4a16_moe_tuning {
   int32_t mfma_tile_m;
   int32_t gemv_units_per_wg;
   int32_t gemv_lanes_per_row;
-  int32_t reserved[2];
+  int32_t w2_fused_max_m;
+  int32_t reserved[1];
 } w4a16_moe_tuning;
 
 /* The built-in tuning for a shape (what NULL selects).  No counterpart in the

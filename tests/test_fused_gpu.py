@@ -57,7 +57,8 @@ def mfma_experts(pkg, ti, E, N, K):
     return {int(e) for e in torch.nonzero(counts > thr).reshape(-1)}
 
 
-def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True, bf16_experts=()):
+def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True, bf16_experts=(),
+           mismatch_max=0.02):
     out32 = out.float().cpu()
     ref = orc.moe_reference(x, w13, w2, s13, s2, tw, ti, group, out_dtype=None)
     rl2 = orc.rel_l2(out32, ref)
@@ -83,7 +84,8 @@ def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True, bf16_e
               f"bf16 mismatch={mismatch:.3%}", flush=True)
         assert trl2 <= 2.5e-3, f"{tag}: tight rel_l2 {trl2}"
         assert excess <= 2e-4, f"{tag}: error beyond rounding {excess}"
-        assert mismatch <= 0.02, f"{tag}: {mismatch:.2%} of outputs differ from bf16(tight)"
+        assert mismatch <= mismatch_max, \
+            f"{tag}: {mismatch:.2%} of outputs differ from bf16(tight)"
     return rl2, mab
 
 
@@ -241,25 +243,31 @@ def test_self_routing_expert_with_many_pairs(pkg, orc, synth, dev, M, topk, E, h
                                               (32, 16, 256, 1024, 32), (256, 10, 3072, 1024, 32),
                                               (8, 1, 256, 256, 128)])
 @pytest.mark.parametrize("drop", [False, True])
+@pytest.mark.parametrize("M", [1, 3])
 def test_one_token_w2_with_combine_bit_identical(pkg, orc, synth, dev, E, topk, K, N, group,
-                                                 drop):
-    """M = 1 runs w2 and the top-k sum in one launch; it must equal the
-    separate GEMV + combine kernels bit for bit (the split dispatch, forced
-    by the tuning, takes that route)."""
+                                                 drop, M):
+    """Few-token calls can run w2 and the top-k sum in one launch (M = 1 by
+    default, more by tuning); it must equal the separate GEMV + combine
+    kernels bit for bit (the split dispatch, forced by the tuning, takes
+    that route)."""
     shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=group)
-    print(f"one-token E={E} topk={topk} K={K} N={N} G={group} drop={drop}", flush=True)
-    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, 1, dev, seed=E + topk)
+    print(f"few-token M={M} E={E} topk={topk} K={K} N={N} G={group} drop={drop}", flush=True)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=E + topk)
     if drop:
         ti = ti.clone()
         ti[0, -1] = E        # out of range: skipped
         if topk > 2:
-            ti[0, 0] = ti[0, 1]  # the same expert twice
-    fused = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group)
+            ti[-1, 0] = ti[-1, 1]  # the same expert twice
+    fused = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group,
+                                    tuning=pkg.Tuning(w2_fused_max_m=M))
     split = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group,
                                     tuning=pkg.Tuning(gemv_only_max_m=0))
     torch.cuda.synchronize()
     assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
-    _check(orc, fused, x, w13, w2, s13, s2, tw, ti, group, "one-token")
+    # The full-size shape's K = 3072 reductions flip a bf16 intermediate now
+    # and then (fp32 summation order); on 3 output rows that is ~2 % of the
+    # outputs one ulp off, the same for the split path (asserted equal above).
+    _check(orc, fused, x, w13, w2, s13, s2, tw, ti, group, "few-token", mismatch_max=0.03)
 
 
 def test_dtypes_and_strides(pkg, orc, synth, dev):
