@@ -55,6 +55,7 @@ struct Layout {
   int64_t max_gemv;   // bound of the GEMV block list / GEMV work items
   int64_t max_items;  // self-routed work items: one per (token, slot) pair
   bool token;         // one token: w2 and the combine in one launch
+  bool partial_bf16;  // PARTIAL holds bf16 rows (else fp32)
   int gemv_max_tokens;
   int tc;
   int upw;
@@ -70,6 +71,11 @@ constexpr int kGemvOnlyMaxM = W4A16_GEMV_ONLY_MAX_M;
 // 48.1 vs 49.1 us (skewed routing 40.9 vs 44.7); at M=8 the experts shared
 // by tokens, read once per token, cancel the saved launch.
 constexpr int kW2FusedMaxM = 4;
+// The reference keeps the top-k-weighted w2 rows in a bf16 buffer
+// (kernels/w4a16_moe.py:311) and sums them in fp32, except for calls of at
+// most this many tokens, which accumulate them in fp32 (:763).  The partial
+// rows here follow the same rounding points.
+constexpr int64_t kFp32PartialMaxM = 4;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -137,6 +143,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
              gemv_route_fits((int)n_tok, (int)E, (int)K, (int)N);
   L->max_items = L->route ? (int64_t)n_tok : 0;
   L->token = L->route && M <= T.w2_fused_max_m && w2_token_fits((int)topk, (int)K, (int)N);
+  L->partial_bf16 = M > kFp32PartialMaxM;
   size_t cur = 0;
   auto put = [&](int field, size_t bytes) {
     L->off[field] = cur;
@@ -147,7 +154,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   put(W4A16_WS_EXPERT_IDS, (size_t)L->nb * sizeof(int32_t));
   put(W4A16_WS_OFFSETS, (size_t)(E + 1) * sizeof(int32_t));
   put(W4A16_WS_INTER, n_tok * (size_t)N * sizeof(uint16_t));
-  put(W4A16_WS_PARTIAL, n_tok * (size_t)K * sizeof(float));
+  put(W4A16_WS_PARTIAL, n_tok * (size_t)K * (L->partial_bf16 ? sizeof(uint16_t) : sizeof(float)));
   put(W4A16_WS_TILES, (size_t)std::max<int64_t>(L->max_tiles, 1) * 4 * sizeof(int32_t));
   put(W4A16_WS_GEMV_BLOCKS, (size_t)std::max<int64_t>(L->max_gemv, 1) * sizeof(int32_t));
   L->total = cur;
@@ -205,7 +212,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   int32_t* eids = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_EXPERT_IDS]);
   int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_OFFSETS]);
   uint16_t* inter = reinterpret_cast<uint16_t*>(ws + L.off[W4A16_WS_INTER]);
-  float* partial = reinterpret_cast<float*>(ws + L.off[W4A16_WS_PARTIAL]);
+  void* partial = ws + L.off[W4A16_WS_PARTIAL];
   const int32_t n_tok = (int32_t)(a.M * a.topk);
 
   (void)hipGetLastError();
@@ -295,6 +302,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.s = static_cast<const uint16_t*>(a.s2);
   g.topk_w = a.topk_w;
   g.out = partial;
+  g.partial_bf16 = L.partial_bf16;
   g.n_out = (int32_t)a.K;
   g.kdim = (int32_t)a.N;
   if (want(2)) {
@@ -310,6 +318,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
     m.s = g.s;
     m.topk_w = a.topk_w;
     m.out = partial;
+    m.partial_bf16 = L.partial_bf16;
     m.n_out = (int32_t)a.K;
     m.kdim = (int32_t)a.N;
     if (launch_w2_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
@@ -318,6 +327,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
 
   CombineLaunch c{};
   c.partial = partial;
+  c.partial_bf16 = L.partial_bf16;
   c.ids = a.ids;
   c.out = static_cast<uint16_t*>(a.out);
   c.ld_out = a.ld_out;

@@ -135,7 +135,8 @@ struct GemvLaunch {
   const int32_t* expert_ids;
   const int32_t* header;   // [0] = num_tokens_post_padded
   const float* topk_w;     // w2 only
-  void* out;               // w13: bf16 inter [n_tok, n_out]; w2: fp32 [n_tok, n_out]
+  void* out;               // w13: bf16 inter [n_tok, n_out]; w2: partial [n_tok, n_out]
+  int32_t partial_bf16;    // w2: partial rows are bf16 (else fp32)
   int32_t n_tok;
   int32_t topk;
   int32_t block;
@@ -180,7 +181,8 @@ struct MfmaLaunch {
   const int4* tiles;       // (expert, first slot, count, 0)
   const int32_t* header;   // [2] = number of tiles
   const float* topk_w;     // w2 only
-  void* out;               // w13: bf16 inter [n_tok, n_out]; w2: fp32 [n_tok, n_out]
+  void* out;               // w13: bf16 inter [n_tok, n_out]; w2: partial [n_tok, n_out]
+  int32_t partial_bf16;    // w2: partial rows are bf16 (else fp32)
   int32_t n_tok;
   int32_t topk;
   int32_t n_out;           // N for w13 (2N weight rows), K for w2
@@ -193,7 +195,8 @@ hipError_t launch_w13_mfma(const MfmaLaunch& a, hipStream_t stream);
 hipError_t launch_w2_mfma(const MfmaLaunch& a, hipStream_t stream);
 
 struct CombineLaunch {
-  const float* partial;    // [M*topk, K]
+  const void* partial;     // [M*topk, K], bf16 or fp32
+  int32_t partial_bf16;
   const int32_t* ids;      // [M, topk]
   uint16_t* out;           // bf16 [M, ld_out]
   int64_t ld_out;

@@ -200,7 +200,7 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
 }
 
 // MODE 0: w13 rows (gate n, up N+n), epilogue SiLU(gate)*up -> bf16 inter.
-// MODE 1: w2 rows, epilogue * topk weight -> fp32 partial.
+// MODE 1: w2 rows, epilogue * topk weight -> partial (bf16, or fp32 at M <= 4).
 // RPL:   output rows per lane (w13: gate+up pairs, so 2*RPL weight rows).
 // PF:    weight loads kept in flight, in group steps.
 // TC:    activation rows staged per pass.
@@ -456,9 +456,15 @@ void gemv_kernel(const GemvLaunch a) {
               out[nb + RG * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
           } else {
             const float wt = a.topk_w[f_mine];
-            float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
+            if (a.partial_bf16) {
+              uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
 #pragma unroll
-            for (int q = 0; q < RPL; ++q) out[nb + RG * q] = v[q] * wt;
+              for (int q = 0; q < RPL; ++q) out[nb + RG * q] = (uint16_t)f32_to_bf16(v[q] * wt);
+            } else {
+              float* out = static_cast<float*>(a.out) + (int64_t)f_mine * a.n_out;
+#pragma unroll
+              for (int q = 0; q < RPL; ++q) out[nb + RG * q] = v[q] * wt;
+            }
           }
         }
       };

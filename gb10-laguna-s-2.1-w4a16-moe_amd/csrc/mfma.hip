@@ -28,7 +28,9 @@
 // lane holds gate and up of the same output column and the epilogue writes
 // bf16(SiLU(gate) * up) -- the reference's rounding point.
 // w2 (MODE 1): the epilogue multiplies by the routing weight and writes the
-// fp32 partial row of the (token, slot) pair.
+// partial row of the (token, slot) pair, rounded to bf16 like the
+// reference's partial buffer (kernels/w4a16_moe.py:311) unless the call
+// keeps fp32 partials (M <= 4, where the reference accumulates in fp32).
 //
 // Workgroup ids are remapped so that the N-tiles of one token tile run on one
 // XCD (consecutive hardware ids round-robin over the 8 XCDs) and share its L2
@@ -369,9 +371,16 @@ __global__ __launch_bounds__(256, TMB == 8 ? 1 : 2) void mfma_kernel(const MfmaL
           out[nt * (kTN / 2) + 32 * wid + j] = (uint16_t)f32_to_bf16(h);
         } else {
           const float wt = a.topk_w[f];
-          float* out = static_cast<float*>(a.out) + (int64_t)f * a.n_out;
-          out[nt * kTN + 64 * wid + j] = acc[m][0][r] * wt;
-          out[nt * kTN + 64 * wid + 32 + j] = acc[m][1][r] * wt;
+          const int col = nt * kTN + 64 * wid + j;
+          if (a.partial_bf16) {
+            uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out;
+            out[col] = (uint16_t)f32_to_bf16(acc[m][0][r] * wt);
+            out[col + 32] = (uint16_t)f32_to_bf16(acc[m][1][r] * wt);
+          } else {
+            float* out = static_cast<float*>(a.out) + (int64_t)f * a.n_out;
+            out[col] = acc[m][0][r] * wt;
+            out[col + 32] = acc[m][1][r] * wt;
+          }
         }
       }
     }

@@ -60,7 +60,8 @@ extern "C" {
                                     [3] GEMV blocks, [4..] reserved              */
 #define W4A16_WS_OFFSETS      3  /* int32 [E+1]           padded expert offsets   */
 #define W4A16_WS_INTER        4  /* bf16  [M*topk, N]     SiLU(gate)*up           */
-#define W4A16_WS_PARTIAL      5  /* fp32  [M*topk, K]     weighted w2 products    */
+#define W4A16_WS_PARTIAL      5  /* bf16  [M*topk, K]     weighted w2 products
+                                    (fp32 when M <= 4)                           */
 #define W4A16_WS_TILES        6  /* int32 [tiles][4]      MFMA work list          */
 #define W4A16_WS_GEMV_BLOCKS  7  /* int32 [blocks]        GEMV work list          */
 #define W4A16_WS_NFIELDS      8
@@ -133,8 +134,11 @@ int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts,
  * Replaces fused_experts_w4a16, kernels/w4a16_moe.py:678-909 (expert sort,
  * w13 dequant-GEMM with SiLU(gate)*up, w2 dequant-GEMM with the top-k
  * weighted combine).  Weights are the unchanged pack-quantized tensors (no
- * repack).  Accumulation is fp32; the w13 output is rounded to bf16 as in the
- * reference; the top-k combine is summed in slot order (deterministic).
+ * repack).  Accumulation is fp32; the rounding points are the reference's:
+ * the w13 output (SiLU(gate)*up) is rounded to bf16, and so is each
+ * top-k-weighted w2 row when M > 4 (the reference's bf16 partial buffer,
+ * :311; at M <= 4 the rows stay fp32, as in its fp32 atomic path, :763).
+ * The top-k combine is summed in fp32 in slot order (deterministic).
  * Requirements: K and N multiples of 32 and of group_size, at most 16384;
  * group_size in {32, 64, 128}; 1 <= topk <= 256; 1 <= E <= 1024;
  * hidden and packed-weight pointers 16-byte aligned; ld_hidden % 8 == 0;

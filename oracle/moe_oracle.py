@@ -27,6 +27,13 @@ Contents and what pins each one (the checks live in tests/test_oracle.py):
   SiLU(gate)*up, top-k-weighted index_add_, bf16 cast), with the dequant done
   inside (it is the timed CPU baseline).  Pinned by a float64 brute force
   (``moe_bruteforce_f64``) on tiny shapes and by linearity/zero-routing cases.
+  ``moe_partials`` returns the same loop's per-(token, slot) rows before the
+  sum (pinned through moe_reference, which sums them).  Its options for the reference kernel's two bf16 rounding points
+  (``round_inter``: SiLU(gate)*up, kernels/w4a16_moe.py:489; ``round_partial``:
+  the top-k-weighted w2 rows, :311, summed in slot order by :638-668) are
+  pinned by the brute force's own scalar rounding at the same points, on
+  inputs where leaving a rounding out moves the result far beyond the
+  fp32-vs-float64 noise.
 
 * ``router_topk_softmax`` -- bench/bench_moe.py:225-230 (``torch.topk`` then
   ``torch.softmax`` over the selected logits), equal logits in ascending
@@ -300,10 +307,67 @@ def _as_u8_tensor(w) -> torch.Tensor:
     return w
 
 
+def _expert_rows(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
+                 topk_weights: torch.Tensor, topk_ids: torch.Tensor, group: int,
+                 exact_weights: bool, round_inter: bool, bf16_weight_experts):
+    """Yield (token_idx, slot_idx, fp32 top-k-weighted w2 rows) per routed expert.
+
+    The per-expert body of run_reference (bench/bench_moe.py:277-303): fp32
+    ``F.linear`` against the dequantized w13, SiLU(gate)*up (silu_and_mul,
+    :271-274), fp32 ``F.linear`` against w2, times the routing weight.
+    """
+    hidden = hidden.detach().cpu()
+    w13b = _as_u8_tensor(w13)
+    w2b = _as_u8_tensor(w2)
+    s13 = w13_scale.detach().cpu()
+    s2 = w2_scale.detach().cpu()
+    assert s13.dtype == torch.bfloat16 and s2.dtype == torch.bfloat16
+    E = w13b.shape[0]
+    N = w13b.shape[1] // 2
+    h = hidden.to(torch.float32)
+    tw = topk_weights.detach().cpu().to(torch.float32)
+    ids = topk_ids.detach().cpu().to(torch.int64)
+    for e in range(E):
+        mask = ids == e
+        if not bool(mask.any()):
+            continue
+        token_idx, slot_idx = mask.nonzero(as_tuple=True)
+        exact = exact_weights and e not in bf16_weight_experts
+        W13 = _dequant_torch(w13b[e], s13[e], group, exact)  # [2N, K]
+        W2 = _dequant_torch(w2b[e], s2[e], group, exact)  # [K, N]
+        y = F.linear(h[token_idx], W13)
+        a = F.silu(y[:, :N]) * y[:, N:]
+        if round_inter:
+            a = a.to(torch.bfloat16).to(torch.float32)
+        yield token_idx, slot_idx, F.linear(a, W2) * tw[token_idx, slot_idx].unsqueeze(-1)
+
+
+def moe_partials(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
+                 topk_weights: torch.Tensor, topk_ids: torch.Tensor, group: int = 32,
+                 *, exact_weights: bool = False, round_inter: bool = False,
+                 bf16_weight_experts=()):
+    """(partial fp32 [M, topk, K], valid bool [M, topk]): the top-k-weighted
+    w2 row of every (token, slot) pair before any rounding, zero where the
+    slot's id is outside [0, E) -- the rows the reference kernel stores in its
+    partial buffer (kernels/w4a16_moe.py:311, :851-888).  Options as in
+    moe_reference."""
+    M, K = hidden.shape
+    topk = topk_ids.shape[1]
+    part = torch.zeros((M, topk, K), dtype=torch.float32)
+    valid = torch.zeros((M, topk), dtype=torch.bool)
+    for token_idx, slot_idx, z in _expert_rows(hidden, w13, w2, w13_scale, w2_scale,
+                                               topk_weights, topk_ids, group, exact_weights,
+                                               round_inter, bf16_weight_experts):
+        part[token_idx, slot_idx] = z
+        valid[token_idx, slot_idx] = True
+    return part, valid
+
+
 def moe_reference(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
                   topk_weights: torch.Tensor, topk_ids: torch.Tensor, group: int = 32,
                   *, exact_weights: bool = False, round_inter: bool = False,
-                  bf16_weight_experts=(), out_dtype=torch.bfloat16) -> torch.Tensor:
+                  round_partial: bool = False, bf16_weight_experts=(),
+                  out_dtype=torch.bfloat16) -> torch.Tensor:
     """PyTorch CPU dequant reference for one MoE layer.
 
     Restates run_reference (bench/bench_moe.py:277-303): for every expert with
@@ -317,43 +381,39 @@ def moe_reference(hidden: torch.Tensor, w13, w2, w13_scale, w2_scale,
     exact_weights is set (a per-expert mix of both rounding points).
     round_inter: round SiLU(gate)*up to bf16 like the reference kernel does
     (kernels/w4a16_moe.py:489).
+    round_partial: round each top-k-weighted w2 row to bf16 and sum the rows
+    of a token in fp32 in slot order from +0.0, leaving out slots whose id is
+    outside [0, E) -- the reference kernel's bf16 partial buffer
+    (kernels/w4a16_moe.py:311) and _moe_sum_kernel (:638-668).
     """
-    hidden = hidden.detach().cpu()
     M, K = hidden.shape
-    w13b = _as_u8_tensor(w13)
-    w2b = _as_u8_tensor(w2)
-    s13 = w13_scale.detach().cpu()
-    s2 = w2_scale.detach().cpu()
-    assert s13.dtype == torch.bfloat16 and s2.dtype == torch.bfloat16
-    E = w13b.shape[0]
-    N = w13b.shape[1] // 2
-    h = hidden.to(torch.float32)
-    tw = topk_weights.detach().cpu().to(torch.float32)
-    ids = topk_ids.detach().cpu().to(torch.int64)
     out = torch.zeros((M, K), dtype=torch.float32)
-    for e in range(E):
-        mask = ids == e
-        if not bool(mask.any()):
-            continue
-        token_idx, slot_idx = mask.nonzero(as_tuple=True)
-        exact = exact_weights and e not in bf16_weight_experts
-        W13 = _dequant_torch(w13b[e], s13[e], group, exact)  # [2N, K]
-        W2 = _dequant_torch(w2b[e], s2[e], group, exact)  # [K, N]
-        y = F.linear(h[token_idx], W13)
-        a = F.silu(y[:, :N]) * y[:, N:]
-        if round_inter:
-            a = a.to(torch.bfloat16).to(torch.float32)
-        z = F.linear(a, W2)
-        out.index_add_(0, token_idx, z * tw[token_idx, slot_idx].unsqueeze(-1))
+    args = (hidden, w13, w2, w13_scale, w2_scale, topk_weights, topk_ids, group)
+    if round_partial:
+        part, valid = moe_partials(*args, exact_weights=exact_weights,
+                                   round_inter=round_inter,
+                                   bf16_weight_experts=bf16_weight_experts)
+        part = part.to(torch.bfloat16).to(torch.float32)
+        for t in range(part.shape[1]):
+            rows = valid[:, t]
+            out[rows] += part[rows, t]
+    else:
+        for token_idx, _, z in _expert_rows(*args, exact_weights, round_inter,
+                                            bf16_weight_experts):
+            out.index_add_(0, token_idx, z)
     return out if out_dtype is None else out.to(out_dtype)
 
 
 def moe_bruteforce_f64(hidden_f32: np.ndarray, w13_deq: np.ndarray, w2_deq: np.ndarray,
-                       topk_weights: np.ndarray, topk_ids: np.ndarray) -> np.ndarray:
+                       topk_weights: np.ndarray, topk_ids: np.ndarray, *,
+                       round_inter: bool = False, round_partial: bool = False) -> np.ndarray:
     """Float64 scalar loops straight from the definition (tiny shapes only).
 
     out[m,k] = sum_t w[m,t] * sum_n W2[e,k,n] * silu(g_n) * u_n,
     g_n = sum_j W13[e,n,j] x[m,j],  u_n = sum_j W13[e,N+n,j] x[m,j].
+    round_inter rounds each silu(g_n) * u_n to bf16, round_partial each
+    w[m,t] * sum_n (...) term (the reference kernel's rounding points,
+    kernels/w4a16_moe.py:489 and :311); the terms are summed in slot order.
     """
     x = np.asarray(hidden_f32, dtype=np.float64)
     M, K = x.shape
@@ -369,9 +429,14 @@ def moe_bruteforce_f64(hidden_f32: np.ndarray, w13_deq: np.ndarray, w2_deq: np.n
                 g = sum(float(w13_deq[e, n, j]) * x[m, j] for j in range(K))
                 u = sum(float(w13_deq[e, N + n, j]) * x[m, j] for j in range(K))
                 a[n] = g / (1.0 + np.exp(-g)) * u
+                if round_inter:
+                    a[n] = float(bf16_round(np.array([a[n]], dtype=np.float32))[0])
             for k in range(K):
-                out[m, k] += float(topk_weights[m, t]) * sum(
+                p = float(topk_weights[m, t]) * sum(
                     float(w2_deq[e, k, n]) * a[n] for n in range(N))
+                if round_partial:
+                    p = float(bf16_round(np.array([p], dtype=np.float32))[0])
+                out[m, k] += p
     return out
 
 

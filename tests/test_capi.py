@@ -75,12 +75,25 @@ def test_workspace_layout(pkg):
         L.WS_EXPERT_IDS: off[L.WS_EXPERT_IDS] + 250 * 4,
         L.WS_OFFSETS: off[L.WS_OFFSETS] + (E + 1) * 4,
         L.WS_INTER: off[L.WS_INTER] + n_tok * N * 2,
-        L.WS_PARTIAL: off[L.WS_PARTIAL] + n_tok * K * 4,
+        L.WS_PARTIAL: off[L.WS_PARTIAL] + n_tok * K * 2,  # bf16 rows above M=4
     }
     spans = sorted((off[f], end) for f, end in ends.items())
     for (a0, a1), (b0, _) in zip(spans, spans[1:]):
         assert a1 <= b0
     assert max(ends.values()) <= size
+
+
+@pytest.mark.parametrize("M,elt", [(1, 4), (4, 4), (5, 2), (64, 2)])
+def test_workspace_partial_dtype(pkg, M, elt):
+    # The weighted w2 rows are fp32 up to M=4 and bf16 above, the reference's
+    # two rounding points (kernels/w4a16_moe.py:311 and :763); the tile list
+    # follows the partial rows directly.
+    L = pkg._lib
+    topk, E, N, K, G = 10, 256, 1024, 3072, 32
+    off = L.workspace_layout(M, topk, E, N, K, G)
+    span = off[L.WS_TILES] - off[L.WS_PARTIAL]
+    need = M * topk * K * elt
+    assert need <= span < need + 256
 
 
 _FUSED_ARGTYPES = 19

@@ -284,3 +284,46 @@ def test_torch_dequant_equals_numpy_dequant(orc, group):
     assert np.array_equal(got, orc.dequant(packed, scales, group))
     got_x = orc.dequant_t(torch.from_numpy(packed), s_t, group, exact=True).numpy()
     assert np.array_equal(got_x.astype(np.float64), orc.dequant_exact(packed, scales, group))
+
+
+# ---------------------------------------------------------------------------
+# the reference kernel's bf16 rounding points (kernels/w4a16_moe.py:489, :311)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("inter,partial", [(True, False), (False, True), (True, True)])
+def test_moe_reference_rounding_points_match_bruteforce(orc, synth, inter, partial):
+    # Independent scalar float64 loops round at the same points; leaving a
+    # rounding out (or putting it elsewhere) differs by bf16 ulps, far above
+    # the fp32-vs-float64 noise of 1e-6.
+    shape, x, w13, w2, s13, s2, tw, ti = _tiny(synth, M=4, topk=3)
+    W13 = orc.dequant(w13, orc._scale_bits(s13), 32)
+    W2 = orc.dequant(w2, orc._scale_bits(s2), 32)
+    xf, twn, tin = x.float().numpy(), tw.numpy(), ti.numpy()
+    got = orc.moe_reference(x, w13, w2, s13, s2, tw, ti, 32, round_inter=inter,
+                            round_partial=partial, out_dtype=None)
+    want = orc.moe_bruteforce_f64(xf, W13, W2, twn, tin, round_inter=inter,
+                                  round_partial=partial)
+    plain = orc.moe_bruteforce_f64(xf, W13, W2, twn, tin)
+    other = orc.moe_bruteforce_f64(xf, W13, W2, twn, tin, round_inter=not inter,
+                                   round_partial=partial)
+    assert orc.rel_l2(got, torch.from_numpy(want)) < 2e-6
+    assert orc.rel_l2(torch.from_numpy(plain), torch.from_numpy(want)) > 1e-4
+    assert orc.rel_l2(torch.from_numpy(other), torch.from_numpy(want)) > 1e-4
+
+
+def test_moe_reference_round_partial_skips_invalid_slots(orc, synth):
+    # A slot routed outside [0, E) contributes nothing: the same as routing it
+    # with weight 0 (whose bf16 partial is +0.0).
+    shape, x, w13, w2, s13, s2, tw, ti = _tiny(synth, M=4, topk=3)
+    bad = ti.clone()
+    bad[1, 2] = -1
+    bad[3, 0] = shape.E
+    zw = tw.clone()
+    zw[1, 2] = 0.0
+    zw[3, 0] = 0.0
+    a = orc.moe_reference(x, w13, w2, s13, s2, tw, bad, 32, round_partial=True,
+                          out_dtype=None)
+    b = orc.moe_reference(x, w13, w2, s13, s2, zw, ti, 32, round_partial=True,
+                          out_dtype=None)
+    assert torch.equal(a, b)
