@@ -169,8 +169,10 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
       if (e >= E) continue;
       const int c = tot[e];
       if (c > thr) {
-        for (int s0 = 0; s0 < c; s0 += a.tile_m)
-          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(a.tile_m, c - s0), 0);
+        const int n_ch = (c + a.tile_m - 1) / a.tile_m;
+        const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
+        for (int s0 = 0; s0 < c; s0 += per)
+          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(per, c - s0), 0);
       } else if (c > 0) {
         a.gemv_blocks[gbase++] = off[e] / B;
       }

@@ -107,7 +107,8 @@ int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   const int tc = t->gemv_tokens_per_pass;
   if (tc != 0 && tc != 1 && tc != 2 && tc != 4) return W4A16_ERR_INVALID_TUNING;
   const int tm = t->mfma_tile_m;
-  if (tm != 0 && tm != kMfmaTileM) return W4A16_ERR_INVALID_TUNING;
+  if (tm != 0 && tm != kMfmaTileMMin && tm != kMfmaTileMMax) return W4A16_ERR_INVALID_TUNING;
+  if (tm != 0) out->tile_m = tm;
   const int upw = t->gemv_units_per_wg;
   if (upw != 0 && upw != 1 && upw != 2 && upw != 4) return W4A16_ERR_INVALID_TUNING;
   out->upw = upw;
@@ -117,8 +118,10 @@ int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   return W4A16_OK;
 }
 
+// mfma_ok = false keeps every expert on the GEMV kernels (the MFMA kernels
+// read the scales in 16-byte pieces and need them 16-byte aligned).
 int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
-                   int64_t group, const Tuning& T, Layout* L) {
+                   int64_t group, const Tuning& T, Layout* L, bool mfma_ok = true) {
   int st = check_gemm_shape(N, K, group);
   if (st) return st;
   st = align_sizes(M, topk, E, W4A16_FUSED_BLOCK_M, &L->em, &L->nb);
@@ -127,7 +130,7 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // MFMA tiles need whole 256-row weight tiles and whole 256-element weight
   // slabs on both GEMMs; small batches cannot give an expert enough pairs to
   // pay for the extra launches.
-  L->mfma = M > T.gemv_only_max_m && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
+  L->mfma = mfma_ok && M > T.gemv_only_max_m && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
   L->gemv_max_tokens = T.gemv_max_tokens;
   L->tc = T.tc;
   L->upw = T.upw;
@@ -184,7 +187,8 @@ int validate(const FusedArgs& a, Layout* L) {
   Tuning T;
   int st = resolve_tuning(a.tuning, &T);
   if (st) return st;
-  st = compute_layout(a.M, a.topk, a.E, a.N, a.K, a.group, T, L);
+  const bool scales16 = aligned(a.s13, 16) && aligned(a.s2, 16);
+  st = compute_layout(a.M, a.topk, a.E, a.N, a.K, a.group, T, L, scales16);
   if (st) return st;
   if (a.M == 0) return W4A16_OK;
   if (!a.hidden || !a.w13 || !a.w2 || !a.s13 || !a.s2 || !a.topk_w || !a.ids ||

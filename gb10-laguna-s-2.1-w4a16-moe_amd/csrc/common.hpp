@@ -95,10 +95,12 @@ __device__ __forceinline__ int wg_exclusive_scan(int v, int* wave_tot, int* tota
 // ---- host launchers (defined next to their kernels) ----------------------
 namespace w4a16 {
 
-// MFMA tile: token slots x weight rows of one workgroup.  The token height
-// is 128 or 256 slots, chosen per call (tile_m of the launches).
-constexpr int kMfmaTileM = 128;
-constexpr int kMfmaTileMMax = 256;
+// MFMA tile: token slots x weight rows of one workgroup.  An expert's pairs
+// are cut into the fewest tiles of at most tile_m slots (192 by default, 128
+// selectable per call), of near-equal size.
+constexpr int kMfmaTileM = 192;
+constexpr int kMfmaTileMMin = 128;
+constexpr int kMfmaTileMMax = 192;
 constexpr int kMfmaTileN = 256;
 
 struct AlignLaunch {
@@ -114,8 +116,9 @@ struct AlignLaunch {
   int32_t* offsets;  // may be null, [E+1]
   int32_t* dropped;  // may be null, [1]
   // Work lists of the fused call (all null for the plain sort).  Experts
-  // with more than gemv_max_tokens pairs get MFMA tiles of up to tile_m
-  // slots; the others keep their single sorted block on the GEMV path.
+  // with more than gemv_max_tokens pairs get ceil(count / tile_m) MFMA tiles
+  // of near-equal size (multiples of 32 slots but the last); the others keep
+  // their single sorted block on the GEMV path.
   // Requires gemv_max_tokens < block.
   int4* tiles;           // [max tiles] (expert, first slot, count, 0)
   int32_t* n_tiles;      // [1]
@@ -189,7 +192,7 @@ struct MfmaLaunch {
   int32_t kdim;
   int32_t group;
   int32_t max_tiles;
-  int32_t tile_m;          // token slots per tile: kMfmaTileM or kMfmaTileMMax
+  int32_t tile_m;          // token slots per tile, at most (128 or 192)
 };
 hipError_t launch_w13_mfma(const MfmaLaunch& a, hipStream_t stream);
 hipError_t launch_w2_mfma(const MfmaLaunch& a, hipStream_t stream);

@@ -4,37 +4,44 @@
 // and _w4a16_moe_w2_kernel (:502-634): per 16-token block x 64-column tile,
 // tl.dot of bf16 activations with bf16(dequantized weights), fp32 accumulate.
 //
-// Here one workgroup (4 waves) owns a tile of up to 128 sorted token slots of
-// one expert x 256 weight rows and walks the reduction axis one 32-element
-// group (one step) at a time:
-//   * packed weights arrive in slabs of 8 groups: 8 lanes read one row's
-//     128-byte line, so every load instruction covers whole lines; a slab is
-//     fetched into registers one slab ahead and parked in LDS (packed, 136 B
-//     per row) together with its scales converted to fp32;
-//   * each wave owns 64 of the 256 weight rows and dequantizes exactly the
-//     MFMA B fragments it needs straight from the packed slab: lane
-//     (j = lane % 32, q = lane / 32) reads the two packed words 2q, 2q+1 of
-//     its row's group and turns each into 8 bf16 values
-//     bf16((code-8) * scale) -- exact in fp32 before the rounding, i.e. the
-//     reference's dequantized weight;
-//   * the gathered activation rows of one group go through a double-buffered
-//     LDS tile (80 B per row), loaded two steps ahead;
-//   * per group each wave issues 16 v_mfma_f32_32x32x16_bf16: 4 token blocks
-//     of 32 x its 2 weight blocks of 32 x 2 halves of the group.  Half `sub`
-//     contracts the k-octets 2q+sub of the group (A and B agree on it), so a
-//     lane's two packed words feed both halves.
+// Here one workgroup (4 waves, one per SIMD) owns a tile of one expert: up to
+// 256 of its sorted (token, slot) pairs x 256 weight rows.  The align kernel
+// cuts an expert into as few such tiles as possible, so every weight is
+// dequantized once per 256 pairs, and the dequantization work per MFMA falls
+// as the expert's pair count grows.
 //
-// w13 (MODE 0): wave w owns gate rows 32w.. and the matching up rows, so each
-// lane holds gate and up of the same output column and the epilogue writes
-// bf16(SiLU(gate) * up) -- the reference's rounding point.
+//   * Each wave owns 64 weight rows (two 32-row MFMA blocks) and reads them
+//     straight from HBM into registers: lane (j, q) of the wave loads the
+//     16-byte group 2t+q of row j for double step t (64 elements of the
+//     reduction axis), four double steps ahead.
+//   * A packed word becomes 8 bf16 weights bf16((c - 8) * s) with 17 VALU
+//     instructions: two nibbles at a time are or-ed into fp16 numbers 1024 + c
+//     (bits 0-3) or 1024 + 16 c (bits 4-7), and v_fma_mix_f32 turns each into
+//     (c - 8) * s exactly, (1024 + c) * s - 1032 s or (1024 + 16 c) * (s / 16)
+//     - 72 s; one v_cvt_pk_bf16_f32 rounds two of them.  The product before
+//     the rounding is exact, so the bf16 weight is the reference's.
+//   * The gathered activation rows of one double step (128 bytes per row) go
+//     through a double-buffered LDS tile, loaded into registers two double
+//     steps ahead.
+//   * MFMA v_mfma_f32_32x32x16_bf16 with the weights as the A operand and the
+//     activations as B: the accumulator of a lane holds one token slot and 16
+//     output rows in runs of 4, so the epilogue stores 4 neighbouring outputs
+//     at a time.
+//   * The accumulators (2 x 8 blocks of 16 fp32) live in the accumulation
+//     registers; one wave per SIMD.
+//
+// w13 (MODE 0): wave w owns gate rows 32w.. of the tile's 128 gate columns
+// and the matching up rows, so each lane holds gate and up of the same output
+// and the epilogue writes bf16(SiLU(gate) * up) -- the reference's rounding
+// point.
 // w2 (MODE 1): the epilogue multiplies by the routing weight and writes the
-// partial row of the (token, slot) pair, rounded to bf16 like the
-// reference's partial buffer (kernels/w4a16_moe.py:311) unless the call
-// keeps fp32 partials (M <= 4, where the reference accumulates in fp32).
+// partial row of the (token, slot) pair, rounded to bf16 like the reference's
+// partial buffer (kernels/w4a16_moe.py:311) unless the call keeps fp32
+// partials (M <= 4, where the reference accumulates in fp32).
 //
-// Workgroup ids are remapped so that the N-tiles of one token tile run on one
-// XCD (consecutive hardware ids round-robin over the 8 XCDs) and share its L2
-// for the activation rows.
+// Workgroup ids are remapped so that the row tiles of one token tile run on
+// one XCD (consecutive hardware ids round-robin over the 8 XCDs) and share
+// its L2 for the gathered activation rows.
 #include <type_traits>
 
 #include "common.hpp"
@@ -43,54 +50,49 @@ namespace w4a16 {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // Native vectors: whole-value copies of HIP's union-based 4-vector structs
 // end up in scratch memory instead of registers.
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kTN = kMfmaTileN;          // weight rows per tile (8 blocks of 32)
-constexpr int kSlab = 4;                 // groups per packed weight slab
-constexpr int kApitch = 32 * 2 + 16;     // bytes per activation row in LDS
-constexpr int kBpitch = kSlab * 16 + 8;  // bytes per packed weight row in LDS
-constexpr int kBbytes = kTN * kBpitch;
-constexpr int kSpitch = kSlab + 1;       // fp32 scales per row in LDS
-constexpr int kSbytes = kTN * kSpitch * 4;
+constexpr int kTN = kMfmaTileN;              // weight rows per tile (8 waves x 32)
+constexpr int kTMMax = kMfmaTileMMax;        // token slots per tile, at most (6 blocks of 32)
+constexpr int kAbuf = kTMMax * 128;          // one LDS activation buffer (128 B rows)
+constexpr int kAbufs = 4;                    // activation buffers (double steps in LDS)
 constexpr int kXcds = 8;
-
-// Token tile of TMB blocks of 32 slots.
-template <int TMB>
-constexpr int lds_bytes() {
-  return 2 * (32 * TMB) * kApitch + kBbytes + kSbytes;
-}
+constexpr int kStepK = 64;                   // reduction elements per double step
+constexpr int kUnroll = 4;                   // double steps per loop iteration
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// 8 codes of one packed word -> 8 bf16 (code - 8) * s in k order.  The
-// masked nibble registers are made opaque so that the byte conversions read
-// them directly (v_cvt_f32_ubyte0..3) instead of re-extracting each nibble.
-__device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
-  uint32_t lo = w & 0x0F0F0F0Fu;         // codes 0,2,4,6
-  uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
-  asm volatile("" : "+v"(lo), "+v"(hi));
-  const float v0 = fmaf((float)(lo & 0xFFu), s, b);
-  const float v1 = fmaf((float)(hi & 0xFFu), s, b);
-  const float v2 = fmaf((float)((lo >> 8) & 0xFFu), s, b);
-  const float v3 = fmaf((float)((hi >> 8) & 0xFFu), s, b);
-  const float v4 = fmaf((float)((lo >> 16) & 0xFFu), s, b);
-  const float v5 = fmaf((float)((hi >> 16) & 0xFFu), s, b);
-  const float v6 = fmaf((float)(lo >> 24), s, b);
-  const float v7 = fmaf((float)(hi >> 24), s, b);
-  const u32x4_t o = {pack_bf16x2(v0, v1), pack_bf16x2(v2, v3), pack_bf16x2(v4, v5),
-                     pack_bf16x2(v6, v7)};
-  return __builtin_bit_cast(bf16x8_t, o);
+// Scale constants of one (row, group): codes at bits 0-3 of an fp16 half use
+// (s, -1032 s), codes at bits 4-7 use (s / 16, -72 s).  Every product and
+// addend is exact in fp32 for scales below 2^118.
+struct GroupScale {
+  float s0, b0, s1, b1;
+};
+
+__device__ __forceinline__ GroupScale group_scale(float s) {
+  return GroupScale{s, -1032.0f * s, 0.0625f * s, -72.0f * s};
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+__device__ __forceinline__ float fma_half(uint32_t h2, int hi, float s, float b) {
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, h2);
+  return fmaf((float)h[hi], s, b);
+}
+
+// SiLU with the hardware reciprocal (1 ulp), well inside the bf16 rounding
+// that follows.
+__device__ __forceinline__ float silu(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
 
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
   const int per = n / kXcds;
@@ -98,22 +100,387 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return (bid % kXcds) * per + bid / kXcds;
 }
 
-// GSHIFT = log2(group / 32), a template parameter so that the scale loads
-// are branch-free (branches around loads make the compiler wait for them).
-// TMB = token blocks of 32 per tile: 4 (two workgroups per CU) or 8 (one;
-// for large batches, where a 256-slot tile holds a whole expert and its
-// weights are dequantized once instead of once per 128 tokens).
-template <int MODE, int GSHIFT, int TMB>
-__global__ __launch_bounds__(256, TMB == 8 ? 1 : 2) void mfma_kernel(const MfmaLaunch a) {
-  constexpr int gshift = GSHIFT;
-  constexpr int kTM = 32 * TMB;
-  constexpr int kAbytes = kTM * kApitch;
-  constexpr int NA = kTM * 4 / 256;  // activation octets per thread per step
+// s_waitcnt with only the vector-memory count: wait until at most n vector
+// memory instructions of this wave are in flight (expcnt and lgkmcnt at their
+// maxima, i.e. not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt lgkmcnt(0): every LDS read of this wave has returned.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt((0xF & 0xF) | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+// Workgroup barrier without a memory fence: the activation tiles arrive by
+// LDS DMA, which the vector-memory counter tracks, so a fence would wait for
+// every load in flight (the weight prefetches too).  Each wave waits for its
+// own DMA with wait_vmcnt first; the memory clobber keeps the compiler from
+// moving LDS accesses across.
+__device__ __forceinline__ void tile_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// A value the compiler cannot see through, in a vector register: the masks
+// of the dequantization then stay operands of one v_and_or_b32.
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
+  return r;
+}
+
+struct Masks {
+  uint32_t lo, hi, magic;
+};
+
+// 8 codes of one packed word (code i in bits 4i) -> 8 bf16 (code - 8) * s in
+// code order.
+__device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, const GroupScale& g,
+                                                 const Masks& mk) {
+  const uint32_t w8 = w >> 8;
+  const uint32_t p0 = (w & mk.lo) | mk.magic;   // codes 0, 4
+  const uint32_t p1 = (w & mk.hi) | mk.magic;   // codes 1, 5 (times 16)
+  const uint32_t p2 = (w8 & mk.lo) | mk.magic;  // codes 2, 6
+  const uint32_t p3 = (w8 & mk.hi) | mk.magic;  // codes 3, 7 (times 16)
+  const float v0 = fma_half(p0, 0, g.s0, g.b0);
+  const float v1 = fma_half(p1, 0, g.s1, g.b1);
+  const float v2 = fma_half(p2, 0, g.s0, g.b0);
+  const float v3 = fma_half(p3, 0, g.s1, g.b1);
+  const float v4 = fma_half(p0, 1, g.s0, g.b0);
+  const float v5 = fma_half(p1, 1, g.s1, g.b1);
+  const float v6 = fma_half(p2, 1, g.s0, g.b0);
+  const float v7 = fma_half(p3, 1, g.s1, g.b1);
+  const u32x4_t o = {pack_bf16x2(v0, v1), pack_bf16x2(v2, v3), pack_bf16x2(v4, v5),
+                     pack_bf16x2(v6, v7)};
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+// LDS of one workgroup (all three rings are filled by LDS DMA):
+//   A  kAbufs buffers of kTMMax rows x 128 bytes: the gathered activation
+//      rows of one double step.  Chunk c (16 bytes) of row r sits at
+//      r * 128 + 16 * (c ^ g(r)), g(r) = (r ^ (r / 8)) % 8, so the lanes
+//      reading one chunk of 8 (or 16) neighbouring rows hit 8 (16) different
+//      16-byte bank groups of a 128-byte (256-byte) bank row.
+//   W  kWslots slots x 8 waves x 1 KB: a wave's packed weights of one double
+//      step, lane l's 16 bytes at l * 16.
+//   S  2 slots x 8 waves x 1 KB: a wave's scales of one loop iteration (8
+//      groups of 32 elements), lane l's bytes at l times the DMA size.
+//   D  1 KB that the surplus activation DMAs of odd token-block counts write
+//      (never read), so that every wave issues the same DMAs per step.
+constexpr int kWaves = 8;
+constexpr int kWslots = 4;
+constexpr int kWslot = kWaves * 1024;
+constexpr int kSslot = kWaves * 1024;
+constexpr int kOffW = kAbufs * kAbuf;
+constexpr int kOffS = kOffW + kWslots * kWslot;
+constexpr int kOffD = kOffS + 2 * kSslot;
+constexpr int kLdsTotal = kOffD + 1024;
+static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
+
+// One tile of MC token blocks (32 slots each).  GSHIFT = log2(group / 32).
+//
+// Wave w owns one 32-row MFMA block of the tile's 256 weight rows: for w13
+// rows 0-15 of the block are gate rows and rows 16-31 the matching up rows
+// (output columns 16 w ..), so accumulator registers r and r + 8 of a lane
+// hold gate and up of one output; for w2 rows 32 w ...  Two waves share each
+// SIMD: one issues MFMAs while the other waits on LDS or dequantizes.
+//
+// Every global load of the main loop is an LDS DMA, issued three double
+// steps ahead, so no vector register waits on memory there.  Issue order per
+// double step t (fixed by scheduling barriers; the prologue issues steps 0-2
+// the same way): [the next iteration's scales when t % 4 == 0] [NA
+// activation DMAs of step t + 3] [1 weight DMA of step t + 3].  At the end of
+// step t each wave waits until its weight DMA of step t + 1 (issued in step
+// t - 2, after that step's activation DMAs) has landed -- the vector-memory
+// count of the instructions behind it is exact below -- and the workgroup
+// barrier then makes every wave's activation rows visible.
+template <int MODE, int GSHIFT, int MC>
+__device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
+                                         const int* s_f, unsigned char* lds) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int j = lane & 31;
+  const int q = lane >> 5;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
+  const int kdim = a.kdim;
+  const int T = kdim / kStepK;  // double steps, a multiple of kUnroll
+  const int gpr = kdim / a.group;
+
+  // ---- activation DMA: the tile's 4 MC DMAs of 1 KB (8 rows each) are dealt
+  // round robin over the 8 waves, NA per wave; DMA k fills rows 8 k .. 8 k + 7
+  // of the buffer: lane l writes row r = 8 k + l / 8 at chunk position l % 8,
+  // so it fetches chunk (l % 8) ^ g(r) of that row.  A wave's surplus DMA
+  // (odd MC) repeats its first one into the dummy region.  Rows of padding
+  // slots read row 0.
+  constexpr int NA = (4 * MC + kWaves - 1) / kWaves;
+  uint32_t a_off[NA];  // byte offset of this lane's source row + chunk
+  int a_dst[NA];       // LDS byte offset within a buffer, or -1: dummy
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    int k = kWaves * i + wid;
+    a_dst[i] = k * 1024;
+    if (k >= 4 * MC) {
+      k = wid;
+      a_dst[i] = -1;
+    }
+    const int r = 8 * k + (lane >> 3);
+    const int f = s_f[r];
+    uint32_t row = 0;
+    if (f < a.n_tok) row = MODE == 0 ? (uint32_t)(f / a.topk) : (uint32_t)f;
+    const int g = (lane >> 3) ^ (k & 7);  // swizzle of row r (see above)
+    a_off[i] = row * (uint32_t)a.ld_act * 2u + (uint32_t)(((lane & 7) ^ g) * 16);
+  }
+  const char* const act = reinterpret_cast<const char*>(a.act);
+  auto dma_a1 = [&](int step, int buf, int i) {
+    const uint32_t koff = (uint32_t)min(step, T - 1) * (kStepK * 2);
+    __builtin_amdgcn_global_load_lds(
+        (global_void*)(act + (a_off[i] + koff)),
+        (lds_void*)(lds + (a_dst[i] < 0 ? kOffD : buf * kAbuf + a_dst[i])), 16, 0, 0);
+  };
+  auto dma_a = [&](int step, int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) dma_a1(step, buf, i);
+  };
+  // Read addresses: row 32 m + j, chunk 4 q + u -> position (4 q + u) ^ g,
+  // g = (j % 8) ^ (j / 8) ^ 4 (m % 2); row 32 (m % 2) + j is in a_rd, the
+  // m / 2 part is an immediate offset.
+  uint32_t a_rd[2][4];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      a_rd[par][u] = (uint32_t)((32 * par + j) * 128 +
+                                16 * ((4 * q + u) ^ (j & 7) ^ (j >> 3) ^ (4 * par)));
+
+  // ---- the weight row of this lane ------------------------------------------
+  int grow;
+  if (MODE == 0) {
+    const int col = nt * (kTN / 2) + 16 * wid + (j & 15);
+    grow = j < 16 ? col : a.n_out + col;  // gate, or the matching up row
+  } else {
+    grow = nt * kTN + 32 * wid + j;
+  }
+  const int64_t e_rows = (int64_t)e * rows_total;
+  const char* const wexp = reinterpret_cast<const char*>(a.w) + e_rows * (kdim / 2);
+  const char* const sexp = reinterpret_cast<const char*>(a.s) + e_rows * gpr * 2;
+  // 16-byte group 2t + q of the row for double step t
+  const uint32_t w_off = (uint32_t)grow * (uint32_t)(kdim / 2) + 16u * q;
+  const uint32_t s_off = (uint32_t)grow * (uint32_t)gpr * 2u;
+  unsigned char* const w_lds = lds + kOffW + wid * 1024;  // + slot * kWslot
+  unsigned char* const s_lds = lds + kOffS + wid * 1024;  // + slot * kSslot
+  auto dma_w = [&](int step, int slot) {
+    const uint32_t koff = (uint32_t)min(step, T - 1) * 32u;
+    __builtin_amdgcn_global_load_lds((global_void*)(wexp + (w_off + koff)),
+                                     (lds_void*)(w_lds + slot * kWslot), 16, 0, 0);
+  };
+  // Scales of one loop iteration (8 groups of 32 elements): 16, 8 or 4 bytes
+  // of the row by group size, naturally aligned (kdim % 256 == 0), as one
+  // 16-byte DMA, two 4-byte DMAs or one 4-byte DMA.  Lanes q = 0 and 1 of a
+  // row load the same bytes.
+  constexpr int kSBytes = GSHIFT == 0 ? 16 : 4;
+  constexpr int kSDmas = GSHIFT == 1 ? 2 : 1;
+  auto dma_s = [&](int it, int slot) {
+    const uint32_t i = (uint32_t)min(it, T / kUnroll - 1);
+#pragma unroll
+    for (int d = 0; d < kSDmas; ++d) {
+      global_void* src = (global_void*)(sexp + (s_off + i * (16u >> GSHIFT) + 4u * d));
+      lds_void* dst = (lds_void*)(s_lds + slot * kSslot + d * 256);
+      if constexpr (GSHIFT == 0)
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+    }
+  };
+  // The scale word (2 bf16) holding group 2 tp + q (in units of 32
+  // elements) of the iteration, and its bf16 half.
+  auto scale_word = [&](int slot, int tp) {
+    const unsigned char* p = s_lds + slot * kSslot + lane * kSBytes;
+    if constexpr (GSHIFT == 0) return *reinterpret_cast<const uint32_t*>(p + 4 * tp);
+    else if constexpr (GSHIFT == 1) return *reinterpret_cast<const uint32_t*>(p + 256 * (tp >> 1));
+    else return *reinterpret_cast<const uint32_t*>(p);
+  };
+  auto scale_value = [&](uint32_t word, int tp) {
+    const int half = GSHIFT == 0 ? q : GSHIFT == 1 ? (tp & 1) : (tp >> 1);
+    const uint32_t bits = half ? (word & 0xFFFF0000u) : (word << 16);
+    return __uint_as_float(bits);
+  };
+
+  const Masks mk{opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
+
+  f32x16_t acc[MC];
+#pragma unroll
+  for (int m = 0; m < MC; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+
+  // Operands of a double step that are read from LDS before it starts (at
+  // the end of the previous step, behind its last MFMAs): the packed weight
+  // words, the scale word and the activation fragments of k-step 0.
+  u32x4_t wq;
+  uint32_t sw;
+  bf16x8_t af[2][MC], bw[2];
+  auto read_a = [&](const unsigned char* abuf, int u, bf16x8_t (&dst)[MC]) {
+#pragma unroll
+    for (int m = 0; m < MC; ++m)
+      dst[m] = *reinterpret_cast<const bf16x8_t*>(abuf + a_rd[m & 1][u] + (m >> 1) * 2 * 32 * 128);
+  };
+  auto read_step_operands = [&](int tp, int sslot) {
+    wq = *reinterpret_cast<const u32x4_t*>(w_lds + tp * kWslot + lane * 16);
+    sw = scale_word(sslot, tp);
+    read_a(lds + tp * kAbuf, 0, af[0]);
+  };
+
+  // Prologue: the scales of iteration 0, then pseudo-steps -3, -2, -1 (the
+  // DMAs of steps 0, 1, 2).
+  dma_s(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+    dma_a(s, s);
+    __builtin_amdgcn_sched_barrier(0);
+    dma_w(s, s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Step 0's data: behind its weight DMA are A(1), W(1), A(2), W(2).
+  wait_vmcnt<2 * NA + 2>();
+  tile_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  read_step_operands(0, 0);
+
+  const int n_it = T / kUnroll;
+  for (int it = 0; it < n_it; ++it) {
+    // One double step; tp = t % 4 is a compile-time constant.
+    auto step = [&](auto tp_c) {
+      constexpr int tp = decltype(tp_c)::value;
+      const int t = it * kUnroll + tp;
+      // This step's DMAs (for step t + 3) are spread over k-steps 0-2 so that
+      // the address unit drains them behind the MFMAs: [scales when tp == 0]
+      // and activation DMA 0 in k-step 0, activation DMA u in k-step u, the
+      // weight DMA in k-step 2 -- still in the order the wait counts assume.
+      // Buffer and slot (t + 3) % 4 were read last for step t - 1, before the
+      // barrier of step t - 1; scale slot (it + 1) % 2 was read last for
+      // step 3 of iteration it - 1.
+      auto issue_dmas = [&](int u) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (tp == 0 && u == 0) dma_s(it + 1, (it + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+          if (i == u || (u == 2 && i > 2)) dma_a1(t + 3, (tp + 3) & 3, i);
+        if (u == 2) dma_w(t + 3, (tp + 3) & 3);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+
+      const unsigned char* const acur = lds + tp * kAbuf;
+      GroupScale gs;
+      auto mfmas = [&](int c, int m0, int m1) {
+#pragma unroll
+        for (int m = m0; m < m1; ++m)
+          acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[c], af[c][m], acc[m], 0, 0, 0);
+      };
+      // Software pipeline over the 4 MFMA k-steps u: the activation
+      // fragments and dequantized weights of u + 1 are produced while the
+      // MFMAs of u run.  An explicit wait for every LDS read issued so far
+      // opens each k-step: the LDS DMAs make the compiler's LDS counter
+      // inexact, so it would otherwise wait for the next fragments' reads
+      // before each MFMA.
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        const int c = u & 1;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        issue_dmas(u);
+        if (u == 0) {
+          gs = group_scale(scale_value(sw, tp));
+          bw[0] = dequant_word(wq[0], gs, mk);
+        }
+        read_a(acur, u + 1, af[c ^ 1]);
+        mfmas(c, 0, MC);
+        bw[c ^ 1] = dequant_word(wq[u + 1], gs, mk);
+        // The next fragments' LDS reads, then each MFMA followed by a share
+        // of the next dequantization.
+        __builtin_amdgcn_sched_group_barrier(0x100, MC, 0);
+#pragma unroll
+        for (int i = 0; i < MC; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, (17 + MC - 1) / MC, 0);
+        }
+      }
+      // k-step 3: its first MFMAs, then the wait for step t+1's DMAs and the
+      // barrier, then step t+1's operand reads behind the remaining MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      wait_lgkmcnt0();
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int kSplit = (MC + 1) / 2;
+      mfmas(1, 0, kSplit);
+      __builtin_amdgcn_sched_barrier(0);
+      // Step t+1's data: behind its weight DMA (step t-2) are step t-1's
+      // [scales] A(t+2) W(t+2) and step t's [scales] A(t+3) W(t+3).
+      wait_vmcnt<2 * NA + 2 + kSDmas * ((tp == 0) + (tp == 1))>();
+      tile_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int tn = (tp + 1) & 3;
+      read_step_operands(tn, tp == 3 ? ((it + 1) & 1) : (it & 1));
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(1, kSplit, MC);
+    };
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+  }
+  // The reads of a step past the last (clamped DMAs, never used) are the
+  // only LDS reads still in flight.
+  wait_lgkmcnt0();
+  // No LDS DMA may still be in flight when the workgroup's LDS is released.
+  wait_vmcnt<0>();
+
+  // Epilogue.  Accumulator register r of a 32x32 block holds weight row
+  // 8 (r / 4) + 4 q + r % 4 of the block and token slot j.
+#pragma unroll
+  for (int m = 0; m < MC; ++m) {
+    const int f = s_f[32 * m + j];
+    if (f >= a.n_tok) continue;
+    if (MODE == 0) {
+      // r < 8: gate column 8 (r / 4) + 4 q + r % 4 of the wave's 16; r + 8:
+      // its up row.
+      uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out +
+                      nt * (kTN / 2) + 16 * wid + 4 * q;
+#pragma unroll
+      for (int i4 = 0; i4 < 2; ++i4) {
+        float h[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) h[c] = silu(acc[m][4 * i4 + c]) * acc[m][8 + 4 * i4 + c];
+        *reinterpret_cast<u32x2_t*>(out + 8 * i4) =
+            u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+      }
+    } else {
+      const float wt = a.topk_w[f];
+      const int64_t base = (int64_t)f * a.n_out + nt * kTN + 32 * wid + 4 * q;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int64_t o = base + 8 * i4;
+        const float v0 = acc[m][4 * i4 + 0] * wt, v1 = acc[m][4 * i4 + 1] * wt;
+        const float v2 = acc[m][4 * i4 + 2] * wt, v3 = acc[m][4 * i4 + 3] * wt;
+        if (a.partial_bf16) {
+          *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(a.out) + o) =
+              u32x2_t{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+        } else {
+          *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.out) + o) = f32x4_t{v0, v1, v2, v3};
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, int GSHIFT>
+__global__ __launch_bounds__(kWaves * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void mfma_kernel(const MfmaLaunch a) {
   extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ int s_f[kTM];
-  unsigned char* const A0 = lds;
-  unsigned char* const Bp = lds + 2 * kAbytes;
-  float* const Sc = reinterpret_cast<float*>(Bp + kBbytes);
+  __shared__ int s_f[kTMMax];
 
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
   const int n_tiles_n = rows_total / kTN;
@@ -126,309 +493,43 @@ __global__ __launch_bounds__(256, TMB == 8 ? 1 : 2) void mfma_kernel(const MfmaL
   const int tile = bid / n_tiles_n;
   const int nt = bid - tile * n_tiles_n;
   const int4 info = a.tiles[tile];
-  const int e = info.x, start = info.y, count = info.z;
+  const int e = info.x, start = info.y;
+  const int count = min(info.z, kTMMax);
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  for (int i = tid; i < kTM; i += 256) s_f[i] = i < count ? a.sorted[start + i] : a.n_tok;
+  for (int i = threadIdx.x; i < kTMMax; i += kWaves * 64)
+    s_f[i] = i < count ? a.sorted[start + i] : a.n_tok;
   __syncthreads();
 
-  const int kdim = a.kdim;
-  const int G = kdim >> 5;  // steps; a multiple of kSlab on this path
-  const int gpr = kdim / a.group;
-  const int nslabs = G / kSlab;
-
-  // ---- activation loads: NA 16-byte octets per thread per step -----------
-  // Rows past the tile's count read row 0 (their results are discarded).
-  const u32x4_t* a_src[NA];
-  int a_lds[NA];
-#pragma unroll
-  for (int i = 0; i < NA; ++i) {
-    const int u = tid + 256 * i;
-    const int row = u >> 2, part = u & 3;
-    const int f = s_f[row];
-    int64_t arow = 0;
-    if (f < a.n_tok) arow = MODE == 0 ? f / a.topk : f;
-    a_src[i] = reinterpret_cast<const u32x4_t*>(a.act + arow * a.ld_act) + part;
-    a_lds[i] = row * kApitch + part * 16;
+  switch ((count + 31) >> 5) {
+    case 1: run_tile<MODE, GSHIFT, 1>(a, e, nt, s_f, lds); break;
+    case 2: run_tile<MODE, GSHIFT, 2>(a, e, nt, s_f, lds); break;
+    case 3: run_tile<MODE, GSHIFT, 3>(a, e, nt, s_f, lds); break;
+    case 4: run_tile<MODE, GSHIFT, 4>(a, e, nt, s_f, lds); break;
+    case 5: run_tile<MODE, GSHIFT, 5>(a, e, nt, s_f, lds); break;
+    case 6: run_tile<MODE, GSHIFT, 6>(a, e, nt, s_f, lds); break;
+    default: break;
   }
-
-  // ---- packed weight slabs: kSlab lanes per row (one group each), rows
-  // (256 / kSlab) * i + tid / kSlab for i < kSlab -------------------------
-  constexpr int kRowsPerPass = 256 / kSlab;
-  auto global_row = [&](int r) {
-    if (MODE == 0) {
-      const int half = kTN / 2;
-      return r < half ? nt * half + r : a.n_out + nt * half + (r - half);
-    }
-    return nt * kTN + r;
-  };
-  const int64_t e_rows = (int64_t)e * rows_total;
-  const char* wexp = reinterpret_cast<const char*>(a.w) + e_rows * G * 16;
-  const int bgrp = tid % kSlab;
-  uint32_t b_off[kSlab];  // byte offset of this thread's rows at group bgrp
-#pragma unroll
-  for (int i = 0; i < kSlab; ++i)
-    b_off[i] = (uint32_t)global_row(kRowsPerPass * i + tid / kSlab) * (uint32_t)G * 16u +
-               (uint32_t)bgrp * 16u;
-  // Scales of row tid: kSlab >> gshift bf16 values per slab.
-  const char* s_row = reinterpret_cast<const char*>(a.s + (e_rows + global_row(tid)) * gpr);
-  static_assert(kSlab == 4, "scale loads below assume 4 groups per slab");
-
-  u32x4_t bs[kSlab];
-  u32x2_t ss;
-  auto load_slab = [&](int slab) {
-    const int sl = min(slab, nslabs - 1);
-    const uint32_t step_off = (uint32_t)sl * kSlab * 16u;
-#pragma unroll
-    for (int i = 0; i < kSlab; ++i)
-      bs[i] = *reinterpret_cast<const u32x4_t*>(wexp + (b_off[i] + step_off));
-    const char* sp = s_row + ((sl * kSlab) >> gshift) * 2;
-    if constexpr (GSHIFT == 0) {
-      ss = *reinterpret_cast<const u32x2_t*>(sp);
-    } else if constexpr (GSHIFT == 1) {
-      ss = u32x2_t{*reinterpret_cast<const uint32_t*>(sp), 0u};
-    } else {
-      ss = u32x2_t{(uint32_t)*reinterpret_cast<const uint16_t*>(sp), 0u};
-    }
-  };
-  auto store_slab = [&]() {
-#pragma unroll
-    for (int i = 0; i < kSlab; ++i) {
-      unsigned char* d = Bp + (kRowsPerPass * i + tid / kSlab) * kBpitch + bgrp * 16;
-      *reinterpret_cast<u32x2_t*>(d) = u32x2_t{bs[i][0], bs[i][1]};
-      *reinterpret_cast<u32x2_t*>(d + 8) = u32x2_t{bs[i][2], bs[i][3]};
-    }
-    float* srow = Sc + tid * kSpitch;
-#pragma unroll
-    for (int g = 0; g < kSlab; ++g) {
-      const int si = g >> gshift;  // scale index within the slab
-      const uint32_t word = ss[si >> 1];
-      srow[g] = bf16_to_f32((si & 1) ? (word >> 16) : (word & 0xFFFFu));
-    }
-  };
-
-  // ---- per-wave fragment geometry -----------------------------------------
-  const int j = lane & 31;
-  const int q = lane >> 5;
-  int nrow[2];  // local weight row of this lane in each of the wave's 2 blocks
-  if (MODE == 0) {
-    nrow[0] = 32 * wid + j;             // gate
-    nrow[1] = kTN / 2 + 32 * wid + j;   // matching up
-  } else {
-    nrow[0] = 64 * wid + j;
-    nrow[1] = 64 * wid + 32 + j;
-  }
-  const int mcount = (count + 31) >> 5;  // active 32-token blocks (workgroup-uniform)
-
-  struct AStage {
-    u32x4_t v[NA];
-  };
-  // Octet i of a thread holds row (tid + 256 i) / 4: only the octets of the
-  // MC active token blocks (rows < 32 MC) are loaded and parked; rows of
-  // inactive blocks are never read by the MFMAs.
-  auto load_a = [&](AStage& st, int step, auto mc_c) {
-    constexpr int NAE = (decltype(mc_c)::value * 32 * 4 + 255) / 256;
-    const int k = min(step, G - 1);
-#pragma unroll
-    for (int i = 0; i < NAE; ++i) st.v[i] = a_src[i][k * 4];
-  };
-  auto store_a = [&](const AStage& st, unsigned char* Ab, auto mc_c) {
-    constexpr int NAE = (decltype(mc_c)::value * 32 * 4 + 255) / 256;
-#pragma unroll
-    for (int i = 0; i < NAE; ++i) *reinterpret_cast<u32x4_t*>(Ab + a_lds[i]) = st.v[i];
-  };
-  // Packed words and scale of group g for this lane's two weight rows.
-  struct BRaw {
-    u32x2_t w[2];
-    float s[2];
-  };
-  auto read_b = [&](BRaw& r, int g) {
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      r.w[n] = *reinterpret_cast<const u32x2_t*>(Bp + nrow[n] * kBpitch + g * 16 + q * 8);
-      r.s[n] = Sc[nrow[n] * kSpitch + g];
-    }
-  };
-  auto dequant_b = [&](const BRaw& r, bf16x8_t (&bfr)[2][2]) {
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const float b = -8.0f * r.s[n];
-      bfr[n][0] = dequant_word(r.w[n][0], r.s[n], b);
-      bfr[n][1] = dequant_word(r.w[n][1], r.s[n], b);
-    }
-  };
-
-  // The main loop for MC active token blocks.  Step s runs its MFMAs with
-  // the B fragments dequantized during step s-1 and, interleaved with them,
-  // dequantizes step s+1's fragments: the matrix core and the vector ALU work
-  // side by side inside one wave.  One barrier per step (the double-buffered
-  // activation tile), one more where a new weight slab is parked.
-  auto run = [&](auto mc_c) {
-    constexpr int MC = decltype(mc_c)::value;
-    f32x16_t acc[MC][2];
-#pragma unroll
-    for (int m = 0; m < MC; ++m)
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.0f;
-
-    // Prologue: slab 0 and A(0) in LDS, A(1), A(2) and slab 1 in flight.
-    // Its loads stay in program order (scheduling barriers), the order the
-    // loop issues them in: the wait counts at the loop head merge the first
-    // entry with the back edge, and a reordered prologue would leave the
-    // loop waiting for every load in flight once per slab.
-    AStage st[2];
-    load_slab(0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(st[0], 0, mc_c);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(st[1], 1, mc_c);
-    __builtin_amdgcn_sched_barrier(0);
-    store_slab();
-    store_a(st[0], A0, mc_c);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(st[0], 2, mc_c);
-    __builtin_amdgcn_sched_barrier(0);
-    load_slab(1);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    bf16x8_t bcur[2][2], bnext[2][2];
-    {
-      BRaw r0;
-      read_b(r0, 0);
-      dequant_b(r0, bcur);
-    }
-
-    for (int slab = 0; slab < nslabs; ++slab) {
-#pragma unroll
-      for (int g = 0; g < kSlab; ++g) {
-        const int step = slab * kSlab + g;
-        unsigned char* const Acur = A0 + (g & 1) * kAbytes;
-        unsigned char* const Anext = A0 + ((g + 1) & 1) * kAbytes;
-        // A(step+1) into the other buffer (read last in step-1, which every
-        // wave has finished), then refill its registers with A(step+3).
-        store_a(st[(g + 1) & 1], Anext, mc_c);
-        load_a(st[(g + 1) & 1], step + 3, mc_c);
-        if (g == kSlab - 1) {
-          // Every wave read this slab's last group in step-1: park the next.
-          // Unconditional, also after the last slab (a clamped reload whose
-          // data is never used): every path to the loop head then carries
-          // the same loads, so the waits there stay exact.
-          store_slab();
-          __syncthreads();
-          load_slab(slab + 2);
-        }
-        // Next step's weight fragments.  Unconditional so that one basic
-        // block holds the reads, the MFMAs and the dequantization (after the
-        // last step this reads a stale but valid group and is never used).
-        BRaw rn;
-        read_b(rn, (g + 1) & (kSlab - 1));
-#pragma unroll
-        for (int m = 0; m < MC; ++m) {
-#pragma unroll
-          for (int sub = 0; sub < 2; ++sub) {
-            const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(
-                Acur + (m * 32 + j) * kApitch + (2 * q + sub) * 16);
-#pragma unroll
-            for (int n = 0; n < 2; ++n)
-              acc[m][n] =
-                  __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bcur[n][sub], acc[m][n], 0, 0, 0);
-          }
-        }
-        dequant_b(rn, bnext);
-        // Interleave: the activation and weight reads first, then each MFMA
-        // followed by a share of the dequantization.
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * MC + 4, 0);
-#pragma unroll
-        for (int i = 0; i < 4 * MC; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 96 / (4 * MC), 0);
-        }
-#pragma unroll
-        for (int n = 0; n < 2; ++n)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) bcur[n][h] = bnext[n][h];
-        __syncthreads();
-      }
-    }
-
-    // Epilogue.  Accumulator register r of a 32x32 block holds row
-    // 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
-#pragma unroll
-    for (int m = 0; m < MC; ++m) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int trow = m * 32 + 8 * (r >> 2) + 4 * q + (r & 3);
-        const int f = s_f[trow];
-        if (f >= a.n_tok) continue;
-        if (MODE == 0) {
-          uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out;
-          const float h = silu(acc[m][0][r]) * acc[m][1][r];
-          out[nt * (kTN / 2) + 32 * wid + j] = (uint16_t)f32_to_bf16(h);
-        } else {
-          const float wt = a.topk_w[f];
-          const int col = nt * kTN + 64 * wid + j;
-          if (a.partial_bf16) {
-            uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out;
-            out[col] = (uint16_t)f32_to_bf16(acc[m][0][r] * wt);
-            out[col + 32] = (uint16_t)f32_to_bf16(acc[m][1][r] * wt);
-          } else {
-            float* out = static_cast<float*>(a.out) + (int64_t)f * a.n_out;
-            out[col] = acc[m][0][r] * wt;
-            out[col + 32] = acc[m][1][r] * wt;
-          }
-        }
-      }
-    }
-  };
-
-  static_assert(TMB == 4 || TMB == 8, "token tile of 4 or 8 blocks");
-  switch (mcount) {
-    case 1: run(std::integral_constant<int, 1>{}); break;
-    case 2: run(std::integral_constant<int, 2>{}); break;
-    case 3: run(std::integral_constant<int, 3>{}); break;
-    case 4: run(std::integral_constant<int, 4>{}); break;
-    default:
-      if constexpr (TMB == 8) {
-        switch (mcount) {
-          case 5: run(std::integral_constant<int, (TMB == 8 ? 5 : 1)>{}); break;
-          case 6: run(std::integral_constant<int, (TMB == 8 ? 6 : 1)>{}); break;
-          case 7: run(std::integral_constant<int, (TMB == 8 ? 7 : 1)>{}); break;
-          default: run(std::integral_constant<int, (TMB == 8 ? 8 : 1)>{}); break;
-        }
-      }
-      break;
-  }
-}
-
-template <int MODE, int TMB>
-hipError_t launch_mfma_m(const MfmaLaunch& a, hipStream_t stream) {
-  const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
-  const int64_t grid = (int64_t)a.max_tiles * (rows_total / kTN);
-  if (grid <= 0) return hipSuccess;
-  const dim3 g((unsigned)grid), b(256);
-  constexpr int lds = lds_bytes<TMB>();
-  switch (a.group) {
-    case 32: hipLaunchKernelGGL((mfma_kernel<MODE, 0, TMB>), g, b, lds, stream, a); break;
-    case 64: hipLaunchKernelGGL((mfma_kernel<MODE, 1, TMB>), g, b, lds, stream, a); break;
-    case 128: hipLaunchKernelGGL((mfma_kernel<MODE, 2, TMB>), g, b, lds, stream, a); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
 }
 
 template <int MODE>
 hipError_t launch_mfma_t(const MfmaLaunch& a, hipStream_t stream) {
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
-  if (rows_total % kTN != 0 || a.kdim % (32 * kSlab) != 0) return hipErrorInvalidValue;
-  switch (a.tile_m) {
-    case kMfmaTileM: return launch_mfma_m<MODE, kMfmaTileM / 32>(a, stream);
+  if (rows_total % kTN != 0 || a.kdim % (kStepK * kUnroll) != 0) return hipErrorInvalidValue;
+  if (a.tile_m < 32 || a.tile_m > kTMMax) return hipErrorInvalidValue;
+  if (reinterpret_cast<uintptr_t>(a.s) % 16 != 0) return hipErrorInvalidValue;
+  // Activation rows are addressed with 32-bit byte offsets.
+  const int64_t act_rows = MODE == 0 ? a.n_tok / a.topk : a.n_tok;
+  if (act_rows * a.ld_act * 2 > (int64_t)UINT32_MAX - 4096) return hipErrorInvalidValue;
+  const int64_t grid = (int64_t)a.max_tiles * (rows_total / kTN);
+  if (grid <= 0) return hipSuccess;
+  const dim3 g((unsigned)grid), b(kWaves * 64);
+  switch (a.group) {
+    case 32: hipLaunchKernelGGL((mfma_kernel<MODE, 0>), g, b, kLdsTotal, stream, a); break;
+    case 64: hipLaunchKernelGGL((mfma_kernel<MODE, 1>), g, b, kLdsTotal, stream, a); break;
+    case 128: hipLaunchKernelGGL((mfma_kernel<MODE, 2>), g, b, kLdsTotal, stream, a); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
 }
 
 }  // namespace

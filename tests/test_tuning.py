@@ -47,7 +47,7 @@ def test_default_tuning_and_workspace_sizes(pkg):
     d = L.default_tuning(16, 10, 256, 1024, 3072, 32)
     assert (d.gemv_only_max_m, d.gemv_max_tokens, d.gemv_tokens_per_pass, d.mfma_tile_m,
             d.gemv_units_per_wg, d.gemv_lanes_per_row, d.w2_fused_max_m) == \
-        (24, 4, 0, 128, 0, 0, 4)
+        (24, 4, 0, 192, 0, 0, 4)
     assert list(d.reserved) == [0]
     for M in (1, 16, 64, 4096):
         base = L.workspace_size(M, 10, 256, 1024, 3072, 32)
@@ -153,7 +153,7 @@ def test_tuning_changes_dispatch(pkg, synth, dev):
         pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, shape.group, tuning=t)
         ws, off = pkg.workspace_tensor(x, ti, w13, w2, shape.group, tuning=t)
         hdr = ws[off[pkg._lib.WS_HEADER]:off[pkg._lib.WS_HEADER] + 16].view(torch.int32).cpu()
-        want_tiles = int(sum((c + 127) // 128 for c in counts if c > thr))
+        want_tiles = int(sum((c + 191) // 192 for c in counts if c > thr))
         want_gemv = int(sum(1 for c in counts if 0 < c <= thr))
         assert int(hdr[2]) == want_tiles, thr
         assert int(hdr[3]) == want_gemv, thr
