@@ -109,10 +109,15 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// s_waitcnt lgkmcnt(0): every LDS read of this wave has returned.
-__device__ __forceinline__ void wait_lgkmcnt0() {
-  __builtin_amdgcn_s_waitcnt((0xF & 0xF) | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+// s_waitcnt lgkmcnt(N): at most N LDS instructions of this wave in flight.
+// The LDS DMAs count in the vector-memory counter only, so the LDS reads of
+// a wave complete in order and N counts the youngest reads exactly.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8));
 }
+__device__ __forceinline__ void wait_lgkmcnt0() { wait_lgkmcnt<0>(); }
 
 // Workgroup barrier without a memory fence: the activation tiles arrive by
 // LDS DMA, which the vector-memory counter tracks, so a fence would wait for
@@ -155,8 +160,30 @@ __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, const GroupScale& g
   return __builtin_bit_cast(bf16x8_t, o);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void global_void;
+// LDS DMA of 16 or 4 bytes per lane: lane l's bytes at global base + voff
+// land at LDS address lds + l * size (a wave-uniform LDS address, in M0).
+// Written as inline assembly so that the compiler's memory counters see no
+// LDS DMA: with one in sight it counts LDS reads out of order and waits for
+// all of them (lgkmcnt(0)) wherever it needs one.  The waits for the DMAs
+// themselves are explicit (wait_vmcnt); the memory clobber keeps LDS accesses
+// in program order around them, and no other code here uses M0.  M0 must be
+// written one wait state before the DMA.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(voff), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(p);
+}
 
 // LDS of one workgroup (all three rings are filled by LDS DMA):
 //   A  kAbufs buffers of kTMMax rows x 128 bytes: the gathered activation
@@ -237,9 +264,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   const char* const act = reinterpret_cast<const char*>(a.act);
   auto dma_a1 = [&](int step, int buf, int i) {
     const uint32_t koff = (uint32_t)min(step, T - 1) * (kStepK * 2);
-    __builtin_amdgcn_global_load_lds(
-        (global_void*)(act + (a_off[i] + koff)),
-        (lds_void*)(lds + (a_dst[i] < 0 ? kOffD : buf * kAbuf + a_dst[i])), 16, 0, 0);
+    lds_dma16(act, a_off[i] + koff,
+              lds_addr(lds + (a_dst[i] < 0 ? kOffD : buf * kAbuf + a_dst[i])));
   };
   auto dma_a = [&](int step, int buf) {
 #pragma unroll
@@ -274,8 +300,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   unsigned char* const s_lds = lds + kOffS + wid * 1024;  // + slot * kSslot
   auto dma_w = [&](int step, int slot) {
     const uint32_t koff = (uint32_t)min(step, T - 1) * 32u;
-    __builtin_amdgcn_global_load_lds((global_void*)(wexp + (w_off + koff)),
-                                     (lds_void*)(w_lds + slot * kWslot), 16, 0, 0);
+    lds_dma16(wexp, w_off + koff, lds_addr(w_lds + slot * kWslot));
   };
   // Scales of one loop iteration (8 groups of 32 elements): 16, 8 or 4 bytes
   // of the row by group size, naturally aligned (kdim % 256 == 0), as one
@@ -287,12 +312,12 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
     const uint32_t i = (uint32_t)min(it, T / kUnroll - 1);
 #pragma unroll
     for (int d = 0; d < kSDmas; ++d) {
-      global_void* src = (global_void*)(sexp + (s_off + i * (16u >> GSHIFT) + 4u * d));
-      lds_void* dst = (lds_void*)(s_lds + slot * kSslot + d * 256);
+      const uint32_t voff = s_off + i * (16u >> GSHIFT) + 4u * d;
+      const uint32_t dst = lds_addr(s_lds + slot * kSslot + d * 256);
       if constexpr (GSHIFT == 0)
-        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+        lds_dma16(sexp, voff, dst);
       else
-        __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+        lds_dma4(sexp, voff, dst);
     }
   };
   // The scale word (2 bf16) holding group 2 tp + q (in units of 32
@@ -322,16 +347,19 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   // words, the scale word and the activation fragments of k-step 0.
   u32x4_t wq;
   uint32_t sw;
-  bf16x8_t af[2][MC], bw[2];
+  bf16x8_t af[4][MC], bw[2];  // af[u]: fragments of k-step u
   auto read_a = [&](const unsigned char* abuf, int u, bf16x8_t (&dst)[MC]) {
 #pragma unroll
     for (int m = 0; m < MC; ++m)
       dst[m] = *reinterpret_cast<const bf16x8_t*>(abuf + a_rd[m & 1][u] + (m >> 1) * 2 * 32 * 128);
   };
+  // The step's weight words and scale word, then its k-step 0 and 1
+  // fragments (into af[0], af[1]).
   auto read_step_operands = [&](int tp, int sslot) {
     wq = *reinterpret_cast<const u32x4_t*>(w_lds + tp * kWslot + lane * 16);
     sw = scale_word(sslot, tp);
     read_a(lds + tp * kAbuf, 0, af[0]);
+    read_a(lds + tp * kAbuf, 1, af[1]);
   };
 
   // Prologue: the scales of iteration 0, then pseudo-steps -3, -2, -1 (the
@@ -379,30 +407,25 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
       auto mfmas = [&](int c, int m0, int m1) {
 #pragma unroll
         for (int m = m0; m < m1; ++m)
-          acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[c], af[c][m], acc[m], 0, 0, 0);
+          acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[c & 1], af[c][m], acc[m], 0, 0, 0);
       };
       // Software pipeline over the 4 MFMA k-steps u: the activation
-      // fragments and dequantized weights of u + 1 are produced while the
-      // MFMAs of u run.  An explicit wait for every LDS read issued so far
-      // opens each k-step: the LDS DMAs make the compiler's LDS counter
-      // inexact, so it would otherwise wait for the next fragments' reads
-      // before each MFMA.
+      // fragments of u + 2 are read and the weights of u + 1 dequantized
+      // while the MFMAs of u run; k-step u waits only for its own fragments
+      // (the compiler's exact LDS counts keep the reads of u + 1 in flight).
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
-        const int c = u & 1;
-        __builtin_amdgcn_sched_barrier(0);
-        wait_lgkmcnt0();
         issue_dmas(u);
         if (u == 0) {
           gs = group_scale(scale_value(sw, tp));
           bw[0] = dequant_word(wq[0], gs, mk);
         }
-        read_a(acur, u + 1, af[c ^ 1]);
-        mfmas(c, 0, MC);
-        bw[c ^ 1] = dequant_word(wq[u + 1], gs, mk);
-        // The next fragments' LDS reads, then each MFMA followed by a share
-        // of the next dequantization.
-        __builtin_amdgcn_sched_group_barrier(0x100, MC, 0);
+        if (u < 2) read_a(acur, u + 2, af[u + 2]);
+        mfmas(u, 0, MC);
+        bw[(u + 1) & 1] = dequant_word(wq[u + 1], gs, mk);
+        // The fragments' LDS reads, then each MFMA followed by a share of
+        // the next dequantization.
+        if (u < 2) __builtin_amdgcn_sched_group_barrier(0x100, MC, 0);
 #pragma unroll
         for (int i = 0; i < MC; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -410,12 +433,11 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
         }
       }
       // k-step 3: its first MFMAs, then the wait for step t+1's DMAs and the
-      // barrier, then step t+1's operand reads behind the remaining MFMAs.
-      __builtin_amdgcn_sched_barrier(0);
-      wait_lgkmcnt0();
+      // barrier, then step t+1's operand reads (into af[0], af[1]) behind the
+      // remaining MFMAs.
       __builtin_amdgcn_sched_barrier(0);
       constexpr int kSplit = (MC + 1) / 2;
-      mfmas(1, 0, kSplit);
+      mfmas(3, 0, kSplit);
       __builtin_amdgcn_sched_barrier(0);
       // Step t+1's data: behind its weight DMA (step t-2) are step t-1's
       // [scales] A(t+2) W(t+2) and step t's [scales] A(t+3) W(t+3).
@@ -425,7 +447,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
       constexpr int tn = (tp + 1) & 3;
       read_step_operands(tn, tp == 3 ? ((it + 1) & 1) : (it & 1));
       __builtin_amdgcn_sched_barrier(0);
-      mfmas(1, kSplit, MC);
+      mfmas(3, kSplit, MC);
     };
     step(std::integral_constant<int, 0>{});
     step(std::integral_constant<int, 1>{});
