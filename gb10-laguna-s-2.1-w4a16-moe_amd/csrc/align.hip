@@ -248,9 +248,224 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   }
 }
 
+// ---- many workgroups (large batches) --------------------------------------
+// The flat index range is cut into chunks of kChunk pairs, one workgroup of
+// kChunk / 64 waves each, so every wave places a single batch of 64 pairs:
+//   align_count_kernel  per chunk, the pairs of each expert -> ctot[chunk][E]
+//                       and the chunk's dropped pairs -> cdrop[chunk];
+//   align_place_kernel  per chunk, the expert totals and the chunk's starting
+//                       rank in every expert (sums over the earlier chunks),
+//                       the padded offsets, and the stable placement of the
+//                       chunk's pairs; workgroup 0 also writes the padding
+//                       sentinels, the block experts, the work lists and the
+//                       scalars.
+// The result is the same function as align_kernel's.
+constexpr int kChunk = 1024;
+constexpr int kChunkWaves = kChunk / 64;
+static_assert(kAlignChunkedMaxE <= kChunk, "one part of the threads covers every expert");
+
+__global__ __launch_bounds__(kChunk) void align_count_kernel(const AlignLaunch a,
+                                                             int32_t* ctot, int32_t* cdrop) {
+  extern __shared__ int32_t hist[];  // [E]
+  const int E = a.num_experts;
+  const int tid = threadIdx.x;
+  for (int i = tid; i <= E; i += kChunk) hist[i] = 0;
+  __syncthreads();
+  const int f = blockIdx.x * kChunk + tid;
+  int drop = 0;
+  if (f < a.n_tok) {
+    const int e = a.ids[f];
+    if (e >= 0 && e < E)
+      atomicAdd(&hist[e], 1);
+    else
+      drop = 1;
+  }
+  // dropped pairs of the chunk: one wave-level ballot count per wave
+  const int wd = __popcll(ballot(drop != 0));
+  __syncthreads();
+  if ((tid & 63) == 0 && wd) atomicAdd(&hist[E], wd);
+  __syncthreads();
+  for (int i = tid; i < E; i += kChunk) ctot[(int64_t)blockIdx.x * E + i] = hist[i];
+  if (tid == 0) cdrop[blockIdx.x] = hist[E];
+}
+
+__global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a,
+                                                             const int32_t* ctot,
+                                                             const int32_t* cdrop) {
+  extern __shared__ int32_t smem[];
+  __shared__ int32_t wave_tot[17];
+  constexpr int nw = kChunkWaves;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int E = a.num_experts;
+  const int B = a.block;
+  const int n_tok = a.n_tok;
+  const int n_chunks = gridDim.x;
+  const int g = blockIdx.x;
+
+  int32_t* cnt = smem;           // [nw][E]
+  int32_t* off = cnt + nw * E;   // [E+1]
+  int32_t* tot = off + E + 1;    // [E]
+
+  // 1. expert totals and this chunk's starting rank in every expert: the
+  // threads split into parts of E, part p summing chunks p, p + parts, ...
+  // (independent loads in flight), combined with LDS atomics
+  for (int i = tid; i < nw * E; i += kChunk) cnt[i] = 0;
+  for (int e = tid; e < E; e += kChunk) tot[e] = off[e] = 0;
+  __syncthreads();
+  {
+    const int parts = max(1, kChunk / E);
+    const int part = tid / E;
+    const int e = tid - part * E;
+    if (part < parts) {
+      int before = 0, all = 0;
+#pragma unroll 4
+      for (int c = part; c < n_chunks; c += parts) {
+        const int v = ctot[(int64_t)c * E + e];
+        before += c < g ? v : 0;
+        all += v;
+      }
+      atomicAdd(&tot[e], all);
+      atomicAdd(&off[e], before);  // parked here until the offsets are known
+    }
+  }
+  __syncthreads();
+
+  // 2. this chunk's per-wave histograms (wave w: pairs 64 w .. of the chunk)
+  const int f = g * kChunk + tid;
+  const int e_me = f < n_tok ? a.ids[f] : -1;
+  const bool ok = f < n_tok && e_me >= 0 && e_me < E;
+  if (ok) atomicAdd(&cnt[wid * E + e_me], 1);
+  __syncthreads();
+
+  // 3. column prefix over the waves, on top of the chunk's starting rank
+  for (int e = tid; e < E; e += kChunk) {
+    int run = off[e];
+    for (int w = 0; w < nw; ++w) {
+      const int c = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+
+  // 4. offsets = exclusive scan of the padded totals
+  const int ipt = (E + kChunk - 1) / kChunk;
+  const int e0 = tid * ipt;
+  int local = 0;
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e < E) local += (tot[e] + B - 1) / B * B;
+  }
+  int total = 0;
+  int excl = block_exclusive_scan(local, wave_tot, &total);
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      off[e] = excl;
+      excl += (tot[e] + B - 1) / B * B;
+    }
+  }
+  if (tid == 0) off[E] = total;
+  __syncthreads();
+
+  // 5. stable placement: lanes routed to the same expert find each other
+  // with ballots over the expert-id bits and take their rank among them
+  int ebits = 0;
+  while ((1 << ebits) < E) ++ebits;
+  uint64_t peers = ballot(ok);
+  for (int bit = 0; bit < ebits; ++bit) {
+    const bool set = ok && ((e_me >> bit) & 1);
+    const uint64_t m = ballot(set);
+    peers &= set ? m : ~m;
+  }
+  if (ok) a.sorted[off[e_me] + cnt[wid * E + e_me] + __popcll(peers & lanemask_lt())] = f;
+  if (g != 0) return;
+
+  // 6. workgroup 0: work lists, sentinels, block experts, scalars
+  if (a.tiles) {
+    const int thr = a.gemv_max_tokens;
+    int nt_local = 0, ng_local = 0;
+    for (int i = 0; i < ipt; ++i) {
+      const int e = e0 + i;
+      if (e < E) {
+        const int c = tot[e];
+        nt_local += c > thr ? (c + a.tile_m - 1) / a.tile_m : 0;
+        ng_local += (c > 0 && c <= thr) ? 1 : 0;
+      }
+    }
+    int n_tiles = 0, n_gemv = 0;
+    int tbase = block_exclusive_scan(nt_local, wave_tot, &n_tiles);
+    int gbase = block_exclusive_scan(ng_local, wave_tot, &n_gemv);
+    for (int i = 0; i < ipt; ++i) {
+      const int e = e0 + i;
+      if (e >= E) continue;
+      const int c = tot[e];
+      if (c > thr) {
+        const int n_ch = (c + a.tile_m - 1) / a.tile_m;
+        const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
+        for (int s0 = 0; s0 < c; s0 += per)
+          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(per, c - s0), 0);
+      } else if (c > 0) {
+        a.gemv_blocks[gbase++] = off[e] / B;
+      }
+    }
+    if (tid == 0) {
+      a.n_tiles[0] = n_tiles;
+      a.n_gemv[0] = n_gemv;
+    }
+  }
+  for (int e = tid; e < E; e += kChunk) {
+    const int p1 = off[e + 1];
+    for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
+  }
+  for (int p = total + tid; p < a.em; p += kChunk) a.sorted[p] = n_tok;
+  for (int b = tid; b < a.n_blocks; b += kChunk) {
+    int eid = -1;
+    const int pos = b * B;
+    if (pos < total) {
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid + 1] > pos)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      eid = lo;
+    }
+    a.expert_ids[b] = eid;
+  }
+  if (a.offsets)
+    for (int e = tid; e <= E; e += kChunk) a.offsets[e] = off[e];
+  if (tid == 0) {
+    a.num_post[0] = total;
+    if (a.dropped) {
+      int d = 0;
+      for (int c = 0; c < n_chunks; ++c) d += cdrop[c];
+      a.dropped[0] = d;
+    }
+  }
+}
+
 }  // namespace
 
+int align_chunks(int n_tok) { return (n_tok + kChunk - 1) / kChunk; }
+
 hipError_t launch_align(const AlignLaunch& a, hipStream_t stream) {
+  if (a.chunk_scratch && a.n_tok >= kAlignChunkedMinPairs && a.num_experts <= kAlignChunkedMaxE) {
+    const int n_chunks = align_chunks(a.n_tok);
+    int32_t* ctot = a.chunk_scratch;
+    int32_t* cdrop = a.chunk_scratch + (size_t)n_chunks * a.num_experts;
+    hipLaunchKernelGGL(align_count_kernel, dim3(n_chunks), dim3(kChunk),
+                       sizeof(int32_t) * ((size_t)a.num_experts + 1), stream, a, ctot, cdrop);
+    const size_t lds = sizeof(int32_t) * ((size_t)kChunkWaves * a.num_experts +
+                                          2 * (size_t)a.num_experts + 1);
+    hipLaunchKernelGGL(align_place_kernel, dim3(n_chunks), dim3(kChunk), lds, stream, a, ctot,
+                       cdrop);
+    return hipGetLastError();
+  }
   const int threads = a.num_experts <= 512 ? 1024 : 512;
   const int nw = threads / 64;
   const size_t lds =

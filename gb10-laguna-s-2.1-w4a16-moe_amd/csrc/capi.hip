@@ -42,6 +42,7 @@ struct Tuning {
   int upw;              // GEMV row slabs per workgroup (0 = launcher's choice)
   int lpr;              // GEMV lanes per weight row (0 = launcher's choice)
   int w2_fused_max_m;   // M at or below this: w2 and the top-k sum as one kernel
+  bool auto_split;      // gemv_max_tokens is the built-in choice (see compute_layout)
 };
 
 struct Layout {
@@ -49,6 +50,9 @@ struct Layout {
   size_t total;
   int64_t em, nb;
   bool mfma;          // heavy experts run on the MFMA kernels
+  bool gemv;          // the GEMV kernels run (they may find no work)
+  bool chunked;       // the sort runs over many workgroups (chunk counts at off_chunks)
+  size_t off_chunks;
   bool route;         // GEMV kernels route themselves; no align kernel
   int tile_m;         // MFMA tile height (slots)
   int64_t max_tiles;  // bound of the MFMA tile list
@@ -76,6 +80,9 @@ constexpr int kW2FusedMaxM = 4;
 // most this many tokens, which accumulate them in fp32 (:763).  The partial
 // rows here follow the same rounding points.
 constexpr int64_t kFp32PartialMaxM = 4;
+// Average (token, slot) pairs per expert from which the built-in split sends
+// every expert to the MFMA kernels (gemv_max_tokens 0, no GEMV launches).
+constexpr int64_t kAllMfmaMinPairs = 32;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -88,7 +95,7 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
 }
 
 Tuning default_tuning() {
-  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0, kW2FusedMaxM};
+  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0, kW2FusedMaxM, true};
 }
 
 // NULL selects the built-in choices; reserved fields must be zero.
@@ -114,6 +121,7 @@ int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   out->upw = upw;
   out->gemv_only_max_m = t->gemv_only_max_m;
   out->gemv_max_tokens = t->gemv_max_tokens;
+  out->auto_split = false;
   out->tc = tc;
   return W4A16_OK;
 }
@@ -132,6 +140,12 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // pay for the extra launches.
   L->mfma = mfma_ok && M > T.gemv_only_max_m && N % kMfmaTileN == 0 && K % kMfmaTileN == 0;
   L->gemv_max_tokens = T.gemv_max_tokens;
+  // Built-in split: once experts average 32 or more pairs, an expert with at
+  // most gemv_max_tokens of them is vanishingly rare, and the two GEMV
+  // launches that would look for one cost more than an MFMA tile for it, so
+  // every expert goes to the MFMA kernels and the GEMV launches are skipped.
+  if (L->mfma && T.auto_split && (int64_t)n_tok >= kAllMfmaMinPairs * E) L->gemv_max_tokens = 0;
+  L->gemv = !L->mfma || L->gemv_max_tokens > 0;
   L->tc = T.tc;
   L->upw = T.upw;
   L->lpr = T.lpr;
@@ -160,6 +174,11 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   put(W4A16_WS_PARTIAL, n_tok * (size_t)K * (L->partial_bf16 ? sizeof(uint16_t) : sizeof(float)));
   put(W4A16_WS_TILES, (size_t)std::max<int64_t>(L->max_tiles, 1) * 4 * sizeof(int32_t));
   put(W4A16_WS_GEMV_BLOCKS, (size_t)std::max<int64_t>(L->max_gemv, 1) * sizeof(int32_t));
+  // Internal (not one of the public fields): the chunk counts of the
+  // many-workgroup sort of large batches.
+  L->chunked = !L->route && (int64_t)n_tok >= kAlignChunkedMinPairs && E <= kAlignChunkedMaxE;
+  L->off_chunks = cur;
+  if (L->chunked) cur = round_up(cur + align_chunk_scratch_ints((int)n_tok, (int)E) * 4, kWsAlign);
   L->total = cur;
   return W4A16_OK;
 }
@@ -237,6 +256,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   al.num_post = header;
   al.offsets = offsets;
   al.dropped = header + 1;
+  al.chunk_scratch = L.chunked ? reinterpret_cast<int32_t*>(ws + L.off_chunks) : nullptr;
   if (L.mfma) {
     al.tiles = tiles;
     al.n_tiles = header + 2;
@@ -286,7 +306,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   m.max_tiles = (int32_t)L.max_tiles;
   m.tile_m = L.tile_m;
 
-  if (want(1) && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (want(1) && L.gemv && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
   if (L.mfma && want(1)) {
     m.act = g.act;
     m.ld_act = g.ld_act;
@@ -310,9 +330,9 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   g.n_out = (int32_t)a.K;
   g.kdim = (int32_t)a.N;
   if (want(2)) {
-    const hipError_t st = L.token
-                              ? launch_w2_token(g, static_cast<uint16_t*>(a.out), a.ld_out, stream)
-                              : launch_w2_gemv(g, stream);
+    const hipError_t st =
+        L.token ? launch_w2_token(g, static_cast<uint16_t*>(a.out), a.ld_out, stream)
+                : (L.gemv ? launch_w2_gemv(g, stream) : hipSuccess);
     if (st != hipSuccess) return W4A16_ERR_HIP;
   }
   if (L.mfma && want(2)) {
@@ -414,7 +434,7 @@ int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts, int64
   if (st) return st;
   *tuning = w4a16_moe_tuning{};
   tuning->gemv_only_max_m = T.gemv_only_max_m;
-  tuning->gemv_max_tokens = T.gemv_max_tokens;
+  tuning->gemv_max_tokens = L.gemv_max_tokens;
   tuning->gemv_tokens_per_pass = T.tc;
   tuning->mfma_tile_m = T.tile_m;
   tuning->gemv_units_per_wg = T.upw;

@@ -126,7 +126,17 @@ struct AlignLaunch {
   int32_t* n_gemv;       // [1]
   int32_t gemv_max_tokens;
   int32_t tile_m;        // MFMA tile height (slots)
+  // Optional scratch of align_chunk_scratch_ints(n_tok, E) int32: with it,
+  // batches of at least kAlignChunkedMinPairs pairs sort in chunks over many
+  // workgroups (two launches) instead of one workgroup.
+  int32_t* chunk_scratch;
 };
+constexpr int kAlignChunkedMinPairs = 8192;
+constexpr int kAlignChunkedMaxE = 512;
+int align_chunks(int n_tok);
+inline size_t align_chunk_scratch_ints(int n_tok, int num_experts) {
+  return (size_t)align_chunks(n_tok) * (num_experts + 1);
+}
 hipError_t launch_align(const AlignLaunch& a, hipStream_t stream);
 
 struct GemvLaunch {

@@ -204,6 +204,9 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *   gemv_max_tokens       larger calls (N, K multiples of 256) send experts
  *                         with more (token, slot) pairs than this (0..15) to
  *                         the MFMA kernels, the others to the GEMV kernels;
+ *                         0 sends every expert to the MFMA kernels and skips
+ *                         the GEMV launches (the built-in choice once experts
+ *                         average 32 or more pairs, 4 below that);
  *   gemv_tokens_per_pass  token rows one GEMV pass reads the weights for:
  *                         0 (the library's choice), 1, 2 or 4;
  *   mfma_tile_m           most (token, slot) pairs of one expert per MFMA

@@ -163,9 +163,27 @@ def test_intermediate_matches_oracle(pkg, orc, synth, dev):
     assert mismatch <= 0.01
 
 
-def test_internal_sort_matches_oracle(pkg, orc, synth, dev):
-    shape = synth.LayerShape(E=64, topk=6, K=256, N=256, group=32)
-    M = 37
+def _expected_work_lists(counts, offs, thr, tile_m):
+    """MFMA tiles and GEMV blocks the align kernel writes: an expert with more
+    than thr pairs gets ceil(c / tile_m) tiles of near-equal size (multiples
+    of 32 slots but the last), every other routed expert its one block."""
+    tiles, gemv = [], []
+    for e, c in enumerate(int(c) for c in counts):
+        if c > thr:
+            n_ch = -(-c // tile_m)
+            per = (-(-c // n_ch) + 31) // 32 * 32
+            tiles += [(e, int(offs[e]) + s0, min(per, c - s0)) for s0 in range(0, c, per)]
+        elif c > 0:
+            gemv.append(int(offs[e]) // 16)
+    return tiles, gemv
+
+
+# (E, topk, K, N, M): the one-workgroup sort, and a batch large enough for the
+# many-workgroup sort (M * topk >= 8192 pairs) whose experts all go to MFMA.
+@pytest.mark.parametrize("E,topk,K,N,M", [(64, 6, 256, 256, 37), (256, 10, 256, 256, 2100),
+                                          (128, 8, 256, 256, 1500)])
+def test_internal_sort_matches_oracle(pkg, orc, synth, dev, E, topk, K, N, M):
+    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=32)
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=9)
     pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
     torch.cuda.synchronize()
@@ -178,19 +196,13 @@ def test_internal_sort_matches_oracle(pkg, orc, synth, dev):
     assert np.array_equal(got_s, want[0])
     assert np.array_equal(got_e, want[1])
     assert hdr[0] == want[2][0] and hdr[1] == 0
-    # work lists: MFMA tiles of <= 128 slots for experts with more than
-    # GEMV_MAX_TOKENS pairs, the single block of every other routed expert
+    got_o = ws[off[3]: off[3] + 4 * (E + 1)].view(torch.int32).cpu().numpy()
+    assert np.array_equal(got_o, want[3])
+    # work lists under the built-in dispatch for this M
+    d = pkg._lib.default_tuning(M, topk, E, N, K, 32)
     hdr = ws[off[2]: off[2] + 16].view(torch.int32).cpu().numpy()
-    thr = pkg._lib.GEMV_MAX_TOKENS
     counts = np.bincount(ti.cpu().numpy().reshape(-1), minlength=shape.E)
-    offs = want[3]
-    tiles, gemv = [], []
-    for e in range(shape.E):
-        c = int(counts[e])
-        if c > thr:
-            tiles += [(e, int(offs[e]) + s0, min(128, c - s0)) for s0 in range(0, c, 128)]
-        elif c > 0:
-            gemv.append(int(offs[e]) // 16)
+    tiles, gemv = _expected_work_lists(counts, want[3], d.gemv_max_tokens, d.mfma_tile_m)
     assert hdr[2] == len(tiles) and hdr[3] == len(gemv)
     got_t = ws[off[6]: off[6] + 16 * len(tiles)].view(torch.int32).cpu().numpy()
     assert [tuple(r[:3]) for r in got_t.reshape(-1, 4)] == tiles
@@ -209,16 +221,20 @@ def test_deterministic(pkg, synth, dev):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_out_of_range_ids_dropped(pkg, orc, synth, dev):
+# M = 8: the one-workgroup sort; M = 2100: the many-workgroup sort, with the
+# dropped ids in different chunks.
+@pytest.mark.parametrize("M", [8, 2100])
+def test_out_of_range_ids_dropped(pkg, orc, synth, dev, M):
     shape = synth.LayerShape(E=16, topk=4, K=256, N=256, group=32)
-    M = 8
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=4)
     ti = ti.clone()
     ti[1, 2] = -1
     ti[5, 0] = shape.E
+    if M > 1000:
+        ti[M - 3, 1] = 1 << 20
     out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
     torch.cuda.synchronize()
-    assert pkg.dropped_pairs(x, ti, w13, w2, 32) == 2
+    assert pkg.dropped_pairs(x, ti, w13, w2, 32) == (2 if M < 1000 else 3)
     _check(orc, out, x, w13, w2, s13, s2, tw, ti, 32, "out-of-range ids",
            bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
 
