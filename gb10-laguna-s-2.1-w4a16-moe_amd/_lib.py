@@ -79,7 +79,7 @@ class TuningStruct(ctypes.Structure):
     _fields_ = [("gemv_only_max_m", ctypes.c_int32), ("gemv_max_tokens", ctypes.c_int32),
                 ("gemv_tokens_per_pass", ctypes.c_int32), ("mfma_tile_m", ctypes.c_int32),
                 ("gemv_units_per_wg", ctypes.c_int32), ("gemv_lanes_per_row", ctypes.c_int32),
-                ("w2_fused_max_m", ctypes.c_int32), ("reserved", ctypes.c_int32 * 1)]
+                ("w2_fused_max_m", ctypes.c_int32), ("mfma_row_tiles", ctypes.c_int32)]
 
 
 def _declare(lib: ctypes.CDLL) -> None:

@@ -4,6 +4,7 @@
 #include <limits.h>
 
 #include <algorithm>
+#include <cmath>
 
 #include "../../include/w4a16_moe.h"
 #include "common.hpp"
@@ -43,6 +44,7 @@ struct Tuning {
   int lpr;              // GEMV lanes per weight row (0 = launcher's choice)
   int w2_fused_max_m;   // M at or below this: w2 and the top-k sum as one kernel
   bool auto_split;      // gemv_max_tokens is the built-in choice (see compute_layout)
+  int row_tiles;        // MFMA row tiles per work item (0 = built-in per GEMM)
 };
 
 struct Layout {
@@ -64,6 +66,8 @@ struct Layout {
   int tc;
   int upw;
   int lpr;
+  int row_tiles_w13;  // MFMA row tiles per work item
+  int row_tiles_w2;
 };
 
 // An expert with more than this many (token, slot) pairs runs on MFMA tiles;
@@ -80,6 +84,38 @@ constexpr int kW2FusedMaxM = 4;
 // most this many tokens, which accumulate them in fp32 (:763).  The partial
 // rows here follow the same rounding points.
 constexpr int64_t kFp32PartialMaxM = 4;
+// Row tiles (256 weight rows) one MFMA workgroup runs in turn for one token
+// tile (a work item): the loads stream on across them, so the latency of a
+// workgroup's first loads is paid once per item, at the price of fewer and
+// longer items.  Built-in choice: the divisor of the row-tile count nearest
+// (in ratio) item_work / (double steps x token blocks per tile), so that an
+// item holds about item_work MFMA block-steps per wave (w13 330, w2 180: w2
+// rows write twice the outputs), with at least two items per CU left for
+// balance.  Measured on MI355X (E=256, top-10,
+// K=3072, N=1024), best per GEMM: M=4096 w13 1 (578 us vs 597 at 2), w2 2
+// (371 vs 394 at 1); M=1024 w13 4 (283 vs 331 at 1), w2 6 (161 vs 211 at
+// 1); skewed M=64 w13 1 (99 vs 118 at 4).  Every choice is bit-identical.
+constexpr double kItemWorkW13 = 330.0;
+constexpr double kItemWorkW2 = 180.0;
+constexpr int64_t kCUs = 256;  // MI355X
+
+int pick_row_tiles(int64_t n_tiles_n, int64_t steps, int64_t n_tok, int64_t E,
+                   double item_work) {
+  const double avg = (double)n_tok / (double)E;
+  const double blocks = std::min(6.0, std::max(1.0, std::ceil(avg / 32.0)));
+  const double want = item_work / ((double)steps * blocks);
+  // items: an estimate of the MFMA tiles (an expert's tile needs > 4 pairs)
+  const int64_t est_tiles = std::max<int64_t>(1, std::min<int64_t>(E, n_tok / 8));
+  int best = 1;
+  double best_d = 1e30;
+  for (int r = 1; r <= n_tiles_n && r <= 16; ++r) {
+    if (n_tiles_n % r) continue;
+    if (r > 1 && est_tiles * (n_tiles_n / r) < 2 * kCUs) break;
+    const double d = std::fabs(std::log((double)r / want));
+    if (d < best_d) best_d = d, best = r;
+  }
+  return best;
+}
 // Average (token, slot) pairs per expert from which the built-in split sends
 // every expert to the MFMA kernels (gemv_max_tokens 0, no GEMV launches).
 constexpr int64_t kAllMfmaMinPairs = 32;
@@ -95,14 +131,15 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
 }
 
 Tuning default_tuning() {
-  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0, kW2FusedMaxM, true};
+  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0, kW2FusedMaxM, true, 0};
 }
 
-// NULL selects the built-in choices; reserved fields must be zero.
+// NULL selects the built-in choices.
 int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   *out = default_tuning();
   if (!t) return W4A16_OK;
-  if (t->reserved[0] != 0) return W4A16_ERR_INVALID_TUNING;
+  if (t->mfma_row_tiles < 0 || t->mfma_row_tiles > 16) return W4A16_ERR_INVALID_TUNING;
+  out->row_tiles = t->mfma_row_tiles;
   if (t->w2_fused_max_m < 0) return W4A16_ERR_INVALID_TUNING;
   if (t->w2_fused_max_m > 0) out->w2_fused_max_m = t->w2_fused_max_m;
   const int lpr = t->gemv_lanes_per_row;
@@ -146,6 +183,10 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // every expert goes to the MFMA kernels and the GEMV launches are skipped.
   if (L->mfma && T.auto_split && (int64_t)n_tok >= kAllMfmaMinPairs * E) L->gemv_max_tokens = 0;
   L->gemv = !L->mfma || L->gemv_max_tokens > 0;
+  L->row_tiles_w13 = T.row_tiles > 0 ? T.row_tiles
+                                      : pick_row_tiles(2 * N / kMfmaTileN, K / 64, n_tok, E, kItemWorkW13);
+  L->row_tiles_w2 = T.row_tiles > 0 ? T.row_tiles
+                                     : pick_row_tiles(K / kMfmaTileN, N / 64, n_tok, E, kItemWorkW2);
   L->tc = T.tc;
   L->upw = T.upw;
   L->lpr = T.lpr;
@@ -316,6 +357,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
     m.out = inter;
     m.n_out = (int32_t)a.N;
     m.kdim = (int32_t)a.K;
+    m.row_tiles = L.row_tiles_w13;
     if (launch_w13_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
   }
   if (ev && hipEventRecord(ev[2], stream) != hipSuccess) return W4A16_ERR_HIP;
@@ -345,6 +387,7 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
     m.partial_bf16 = L.partial_bf16;
     m.n_out = (int32_t)a.K;
     m.kdim = (int32_t)a.N;
+    m.row_tiles = L.row_tiles_w2;
     if (launch_w2_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
   }
   if (ev && hipEventRecord(ev[3], stream) != hipSuccess) return W4A16_ERR_HIP;

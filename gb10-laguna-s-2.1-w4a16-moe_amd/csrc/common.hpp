@@ -203,6 +203,7 @@ struct MfmaLaunch {
   int32_t group;
   int32_t max_tiles;
   int32_t tile_m;          // token slots per tile, at most (128 or 192)
+  int32_t row_tiles;       // row tiles (kMfmaTileN rows) one workgroup runs in turn
 };
 hipError_t launch_w13_mfma(const MfmaLaunch& a, hipStream_t stream);
 hipError_t launch_w2_mfma(const MfmaLaunch& a, hipStream_t stream);

@@ -225,7 +225,7 @@ static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
 // count of the instructions behind it is exact below -- and the workgroup
 // barrier then makes every wave's activation rows visible.
 template <int MODE, int GSHIFT, int MC>
-__device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
+__device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, int nrt,
                                          const int* s_f, unsigned char* lds) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -234,8 +234,17 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
   const int kdim = a.kdim;
-  const int T = kdim / kStepK;  // double steps, a multiple of kUnroll
+  const int T = kdim / kStepK;  // double steps of one row tile, a multiple of kUnroll
+  const int IT = T / kUnroll;    // loop iterations of one row tile
+  const int GT = nrt * T;        // double steps of the item (nrt row tiles)
   const int gpr = kdim / a.group;
+  // Row tile of global double step gs in [0, GT): the DMAs run up to three
+  // steps ahead, i.e. at most one row tile past rt_cur (T >= kUnroll).
+  auto split_step = [&](int gs, int rt_cur, int& rt, int& k) {
+    const int gc = min(gs, GT - 1);
+    rt = gc >= (rt_cur + 1) * T ? rt_cur + 1 : rt_cur;
+    k = gc - rt * T;
+  };
 
   // ---- activation DMA: the tile's 4 MC DMAs of 1 KB (8 rows each) are dealt
   // round robin over the 8 waves, NA per wave; DMA k fills rows 8 k .. 8 k + 7
@@ -262,14 +271,15 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
     a_off[i] = row * (uint32_t)a.ld_act * 2u + (uint32_t)(((lane & 7) ^ g) * 16);
   }
   const char* const act = reinterpret_cast<const char*>(a.act);
-  auto dma_a1 = [&](int step, int buf, int i) {
-    const uint32_t koff = (uint32_t)min(step, T - 1) * (kStepK * 2);
+  // The item's row tiles share the activation rows: local step k of any.
+  auto dma_a1 = [&](int k, int buf, int i) {
+    const uint32_t koff = (uint32_t)k * (kStepK * 2);
     lds_dma16(act, a_off[i] + koff,
               lds_addr(lds + (a_dst[i] < 0 ? kOffD : buf * kAbuf + a_dst[i])));
   };
-  auto dma_a = [&](int step, int buf) {
+  auto dma_a = [&](int k, int buf) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) dma_a1(step, buf, i);
+    for (int i = 0; i < NA; ++i) dma_a1(k, buf, i);
   };
   // Read addresses: row 32 m + j, chunk 4 q + u -> position (4 q + u) ^ g,
   // g = (j % 8) ^ (j / 8) ^ 4 (m % 2); row 32 (m % 2) + j is in a_rd, the
@@ -283,12 +293,14 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
                                 16 * ((4 * q + u) ^ (j & 7) ^ (j >> 3) ^ (4 * par)));
 
   // ---- the weight row of this lane ------------------------------------------
+  // Row tile nt0 + rt moves every row by kTN / 2 (w13: gate and up) or kTN.
+  constexpr int kRowsPerTile = MODE == 0 ? kTN / 2 : kTN;
   int grow;
   if (MODE == 0) {
-    const int col = nt * (kTN / 2) + 16 * wid + (j & 15);
+    const int col = nt0 * (kTN / 2) + 16 * wid + (j & 15);
     grow = j < 16 ? col : a.n_out + col;  // gate, or the matching up row
   } else {
-    grow = nt * kTN + 32 * wid + j;
+    grow = nt0 * kTN + 32 * wid + j;
   }
   const int64_t e_rows = (int64_t)e * rows_total;
   const char* const wexp = reinterpret_cast<const char*>(a.w) + e_rows * (kdim / 2);
@@ -298,8 +310,10 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   const uint32_t s_off = (uint32_t)grow * (uint32_t)gpr * 2u;
   unsigned char* const w_lds = lds + kOffW + wid * 1024;  // + slot * kWslot
   unsigned char* const s_lds = lds + kOffS + wid * 1024;  // + slot * kSslot
-  auto dma_w = [&](int step, int slot) {
-    const uint32_t koff = (uint32_t)min(step, T - 1) * 32u;
+  const uint32_t w_tile = (uint32_t)kRowsPerTile * (uint32_t)(kdim / 2);
+  const uint32_t s_tile = (uint32_t)kRowsPerTile * (uint32_t)gpr * 2u;
+  auto dma_w = [&](int rt, int k, int slot) {
+    const uint32_t koff = (uint32_t)rt * w_tile + (uint32_t)k * 32u;
     lds_dma16(wexp, w_off + koff, lds_addr(w_lds + slot * kWslot));
   };
   // Scales of one loop iteration (8 groups of 32 elements): 16, 8 or 4 bytes
@@ -308,11 +322,14 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   // row load the same bytes.
   constexpr int kSBytes = GSHIFT == 0 ? 16 : 4;
   constexpr int kSDmas = GSHIFT == 1 ? 2 : 1;
-  auto dma_s = [&](int it, int slot) {
-    const uint32_t i = (uint32_t)min(it, T / kUnroll - 1);
+  // Scales of global iteration git (clamped to the item's last).
+  auto dma_s = [&](int git, int slot) {
+    const int gc = min(git, nrt * IT - 1);
+    const int rt = gc / IT;  // once per iteration
+    const uint32_t i = (uint32_t)(gc - rt * IT);
 #pragma unroll
     for (int d = 0; d < kSDmas; ++d) {
-      const uint32_t voff = s_off + i * (16u >> GSHIFT) + 4u * d;
+      const uint32_t voff = s_off + (uint32_t)rt * s_tile + i * (16u >> GSHIFT) + 4u * d;
       const uint32_t dst = lds_addr(s_lds + slot * kSslot + d * 256);
       if constexpr (GSHIFT == 0)
         lds_dma16(sexp, voff, dst);
@@ -362,15 +379,68 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
     read_a(lds + tp * kAbuf, 1, af[1]);
   };
 
+  // Token rows of the accumulator columns: slot 32 m + j, its routing
+  // weight (w2), loaded before the DMAs start so that no load with a register
+  // result waits behind them.
+  int f_out[MC];
+  float wt_out[MC];
+#pragma unroll
+  for (int m = 0; m < MC; ++m) {
+    f_out[m] = s_f[32 * m + j];
+    wt_out[m] = (MODE == 1 && f_out[m] < a.n_tok) ? a.topk_w[f_out[m]] : 0.0f;
+  }
+
+  // Output of row tile nt.  Accumulator register r of a 32x32 block holds
+  // weight row 8 (r / 4) + 4 q + r % 4 of the wave's block and token slot j.
+  auto write_out = [&](int nt) {
+#pragma unroll
+    for (int m = 0; m < MC; ++m) {
+      const int f = f_out[m];
+      if (f >= a.n_tok) continue;
+      if (MODE == 0) {
+        // r < 8: gate column 8 (r / 4) + 4 q + r % 4 of the wave's 16; r + 8:
+        // its up row.
+        uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out +
+                        nt * (kTN / 2) + 16 * wid + 4 * q;
+#pragma unroll
+        for (int i4 = 0; i4 < 2; ++i4) {
+          float h[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) h[c] = silu(acc[m][4 * i4 + c]) * acc[m][8 + 4 * i4 + c];
+          *reinterpret_cast<u32x2_t*>(out + 8 * i4) =
+              u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+        }
+      } else {
+        const float wt = wt_out[m];
+        const int64_t base = (int64_t)f * a.n_out + nt * kTN + 32 * wid + 4 * q;
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int64_t o = base + 8 * i4;
+          const float v0 = acc[m][4 * i4 + 0] * wt, v1 = acc[m][4 * i4 + 1] * wt;
+          const float v2 = acc[m][4 * i4 + 2] * wt, v3 = acc[m][4 * i4 + 3] * wt;
+          if (a.partial_bf16) {
+            *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(a.out) + o) =
+                u32x2_t{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+          } else {
+            *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.out) + o) =
+                f32x4_t{v0, v1, v2, v3};
+          }
+        }
+      }
+    }
+  };
+
   // Prologue: the scales of iteration 0, then pseudo-steps -3, -2, -1 (the
   // DMAs of steps 0, 1, 2).
   dma_s(0, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < 3; ++s) {
-    dma_a(s, s);
+    int rt, k;
+    split_step(s, 0, rt, k);
+    dma_a(k, s);
     __builtin_amdgcn_sched_barrier(0);
-    dma_w(s, s);
+    dma_w(rt, k, s);
     __builtin_amdgcn_sched_barrier(0);
   }
   // Step 0's data: behind its weight DMA are A(1), W(1), A(2), W(2).
@@ -379,12 +449,18 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
   __builtin_amdgcn_sched_barrier(0);
   read_step_operands(0, 0);
 
-  const int n_it = T / kUnroll;
+  // Global iterations over the item's row tiles; every IT of them finish a
+  // row tile, whose outputs are written before the next one accumulates.
+  // The DMA stream runs on across the row-tile boundary.
+  const int n_it = nrt * IT;
+  int rt_cur = 0;
   for (int it = 0; it < n_it; ++it) {
     // One double step; tp = t % 4 is a compile-time constant.
     auto step = [&](auto tp_c) {
       constexpr int tp = decltype(tp_c)::value;
       const int t = it * kUnroll + tp;
+      int rt_d, k_d;  // row tile and local step of this step's DMAs (t + 3)
+      split_step(t + 3, rt_cur, rt_d, k_d);
       // This step's DMAs (for step t + 3) are spread over k-steps 0-2 so that
       // the address unit drains them behind the MFMAs: [scales when tp == 0]
       // and activation DMA 0 in k-step 0, activation DMA u in k-step u, the
@@ -397,8 +473,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
         if (tp == 0 && u == 0) dma_s(it + 1, (it + 1) & 1);
 #pragma unroll
         for (int i = 0; i < NA; ++i)
-          if (i == u || (u == 2 && i > 2)) dma_a1(t + 3, (tp + 3) & 3, i);
-        if (u == 2) dma_w(t + 3, (tp + 3) & 3);
+          if (i == u || (u == 2 && i > 2)) dma_a1(k_d, (tp + 3) & 3, i);
+        if (u == 2) dma_w(rt_d, k_d, (tp + 3) & 3);
         __builtin_amdgcn_sched_barrier(0);
       };
 
@@ -453,49 +529,20 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt,
     step(std::integral_constant<int, 1>{});
     step(std::integral_constant<int, 2>{});
     step(std::integral_constant<int, 3>{});
+    if (it + 1 == (rt_cur + 1) * IT) {
+      write_out(nt0 + rt_cur);
+#pragma unroll
+      for (int m = 0; m < MC; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+      ++rt_cur;
+    }
   }
   // The reads of a step past the last (clamped DMAs, never used) are the
   // only LDS reads still in flight.
   wait_lgkmcnt0();
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   wait_vmcnt<0>();
-
-  // Epilogue.  Accumulator register r of a 32x32 block holds weight row
-  // 8 (r / 4) + 4 q + r % 4 of the block and token slot j.
-#pragma unroll
-  for (int m = 0; m < MC; ++m) {
-    const int f = s_f[32 * m + j];
-    if (f >= a.n_tok) continue;
-    if (MODE == 0) {
-      // r < 8: gate column 8 (r / 4) + 4 q + r % 4 of the wave's 16; r + 8:
-      // its up row.
-      uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out +
-                      nt * (kTN / 2) + 16 * wid + 4 * q;
-#pragma unroll
-      for (int i4 = 0; i4 < 2; ++i4) {
-        float h[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) h[c] = silu(acc[m][4 * i4 + c]) * acc[m][8 + 4 * i4 + c];
-        *reinterpret_cast<u32x2_t*>(out + 8 * i4) =
-            u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-      }
-    } else {
-      const float wt = a.topk_w[f];
-      const int64_t base = (int64_t)f * a.n_out + nt * kTN + 32 * wid + 4 * q;
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int64_t o = base + 8 * i4;
-        const float v0 = acc[m][4 * i4 + 0] * wt, v1 = acc[m][4 * i4 + 1] * wt;
-        const float v2 = acc[m][4 * i4 + 2] * wt, v3 = acc[m][4 * i4 + 3] * wt;
-        if (a.partial_bf16) {
-          *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(a.out) + o) =
-              u32x2_t{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-        } else {
-          *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.out) + o) = f32x4_t{v0, v1, v2, v3};
-        }
-      }
-    }
-  }
 }
 
 template <int MODE, int GSHIFT>
@@ -506,14 +553,18 @@ void mfma_kernel(const MfmaLaunch a) {
 
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
   const int n_tiles_n = rows_total / kTN;
+  // A work item is up to row_tiles consecutive row tiles of one token tile.
+  const int per_item = a.row_tiles;
+  const int items_per_tile = (n_tiles_n + per_item - 1) / per_item;
   // The grid is sized for the most tiles a routing can produce; the align
   // kernel wrote the real count.  Workgroups past it leave at once, and the
   // XCD remap runs over the real ones so that every XCD gets its share.
-  const int n_active = a.header[2] * n_tiles_n;
+  const int n_active = a.header[2] * items_per_tile;
   if ((int)blockIdx.x >= n_active) return;
   const int bid = xcd_remap(blockIdx.x, n_active);
-  const int tile = bid / n_tiles_n;
-  const int nt = bid - tile * n_tiles_n;
+  const int tile = bid / items_per_tile;
+  const int nt0 = (bid - tile * items_per_tile) * per_item;
+  const int nrt = min(per_item, n_tiles_n - nt0);
   const int4 info = a.tiles[tile];
   const int e = info.x, start = info.y;
   const int count = min(info.z, kTMMax);
@@ -523,12 +574,12 @@ void mfma_kernel(const MfmaLaunch a) {
   __syncthreads();
 
   switch ((count + 31) >> 5) {
-    case 1: run_tile<MODE, GSHIFT, 1>(a, e, nt, s_f, lds); break;
-    case 2: run_tile<MODE, GSHIFT, 2>(a, e, nt, s_f, lds); break;
-    case 3: run_tile<MODE, GSHIFT, 3>(a, e, nt, s_f, lds); break;
-    case 4: run_tile<MODE, GSHIFT, 4>(a, e, nt, s_f, lds); break;
-    case 5: run_tile<MODE, GSHIFT, 5>(a, e, nt, s_f, lds); break;
-    case 6: run_tile<MODE, GSHIFT, 6>(a, e, nt, s_f, lds); break;
+    case 1: run_tile<MODE, GSHIFT, 1>(a, e, nt0, nrt, s_f, lds); break;
+    case 2: run_tile<MODE, GSHIFT, 2>(a, e, nt0, nrt, s_f, lds); break;
+    case 3: run_tile<MODE, GSHIFT, 3>(a, e, nt0, nrt, s_f, lds); break;
+    case 4: run_tile<MODE, GSHIFT, 4>(a, e, nt0, nrt, s_f, lds); break;
+    case 5: run_tile<MODE, GSHIFT, 5>(a, e, nt0, nrt, s_f, lds); break;
+    case 6: run_tile<MODE, GSHIFT, 6>(a, e, nt0, nrt, s_f, lds); break;
     default: break;
   }
 }
@@ -542,7 +593,9 @@ hipError_t launch_mfma_t(const MfmaLaunch& a, hipStream_t stream) {
   // Activation rows are addressed with 32-bit byte offsets.
   const int64_t act_rows = MODE == 0 ? a.n_tok / a.topk : a.n_tok;
   if (act_rows * a.ld_act * 2 > (int64_t)UINT32_MAX - 4096) return hipErrorInvalidValue;
-  const int64_t grid = (int64_t)a.max_tiles * (rows_total / kTN);
+  if (a.row_tiles < 1) return hipErrorInvalidValue;
+  const int64_t grid =
+      (int64_t)a.max_tiles * ((rows_total / kTN + a.row_tiles - 1) / a.row_tiles);
   if (grid <= 0) return hipSuccess;
   const dim3 g((unsigned)grid), b(kWaves * 64);
   switch (a.group) {

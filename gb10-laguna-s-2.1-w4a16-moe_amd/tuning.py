@@ -38,6 +38,7 @@ class Tuning:
     gemv_units_per_wg: int = 0
     gemv_lanes_per_row: int = 0
     w2_fused_max_m: int = 0
+    mfma_row_tiles: int = 0
 
     def to_struct(self) -> _lib.TuningStruct:
         t = _lib.TuningStruct()
@@ -48,6 +49,7 @@ class Tuning:
         t.gemv_units_per_wg = int(self.gemv_units_per_wg)
         t.gemv_lanes_per_row = int(self.gemv_lanes_per_row)
         t.w2_fused_max_m = int(self.w2_fused_max_m)
+        t.mfma_row_tiles = int(self.mfma_row_tiles)
         return t
 
     @classmethod

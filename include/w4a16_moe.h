@@ -220,7 +220,12 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *                         and the top-k sum as one kernel (an expert shared
  *                         by several tokens is then read once per token):
  *                         0 (the library's choice: 4) or a token count.
- * reserved must be zero.  Every choice computes the same function; the
+ *   mfma_row_tiles        256-row weight tiles of one token tile that one MFMA
+ *                         workgroup runs in turn, its loads streaming on across
+ *                         them: 0 (the library's choice per GEMM, by the
+ *                         work per tile) or 1..16 for both (results are
+ *                         bit-identical for every value).
+ * Every choice computes the same function; the
  * GEMV and MFMA kernels differ only in rounding (within the tolerance of
  * fused_experts).  A NULL tuning selects w4a16_moe_default_tuning's values.
  */
@@ -232,7 +237,7 @@ typedef struct w4a16_moe_tuning {
   int32_t gemv_units_per_wg;
   int32_t gemv_lanes_per_row;
   int32_t w2_fused_max_m;
-  int32_t reserved[1];
+  int32_t mfma_row_tiles;
 } w4a16_moe_tuning;
 
 /* The built-in tuning for a shape (what NULL selects).  No counterpart in the

@@ -103,7 +103,7 @@ def _check(orc, out, x, w13, w2, s13, s2, tw, ti, group, tag, tight=True, bf16_e
 
 SMALL = [
     # E, topk, K, N, group, M
-    (4, 2, 512, 256, 32, 300),    # MFMA: two 128-slot tiles per expert
+    (4, 2, 512, 256, 32, 300),    # MFMA: an expert's pairs in one or two tiles
     (8, 4, 1024, 512, 64, 150),   # MFMA with group 64
     (6, 3, 256, 256, 128, 97),    # MFMA with group 128
     (8, 4, 1024, 384, 64, 150),   # N not a multiple of 256: GEMV only, many tokens
@@ -116,6 +116,9 @@ SMALL = [
     (16, 4, 512, 512, 128, 9),
     (4, 4, 256, 256, 32, 40),   # every expert gets many tokens (multi-pass staging)
     (256, 10, 256, 256, 32, 2),
+    # MFMA work items of several row tiles, the last one short (w2: 3 + 1
+    # row tiles), and an expert split into two 192-slot tiles
+    (4, 2, 1024, 512, 32, 400),
 ]
 
 
@@ -413,3 +416,18 @@ def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
     rl2, mab = _check(orc, out, x.cpu(), w13.cpu(), w2.cpu(), s13.cpu(), s2.cpu(),
                       tw.cpu(), ti.cpu(), 32, "reference magnitudes")
     assert mab <= MAX_ABS_MAX
+
+
+@pytest.mark.parametrize("E,topk,K,N,M", [(256, 10, 3072, 1024, 640), (4, 2, 1024, 512, 400)])
+def test_mfma_row_tiles_bit_identical(pkg, synth, dev, E, topk, K, N, M):
+    """A work item of several row tiles streams its loads on across them but
+    accumulates every row tile exactly as a one-tile item does."""
+    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=32)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=21)
+    outs = []
+    for rt in (1, 2, 3, 5, 16):
+        t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=0, mfma_row_tiles=rt)
+        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=t))
+    torch.cuda.synchronize()
+    for rt, o in zip((2, 3, 5, 16), outs[1:]):
+        assert torch.equal(o, outs[0]), f"row tiles {rt}"
