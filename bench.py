@@ -63,8 +63,10 @@ MALL_BYTES = 256 * 2**20       # Infinity Cache
 REFERENCE_GBS_M16 = 226.3
 STAGES = ("align", "w13", "w2", "combine")
 CALIB_BYTES = 512 * 2**20       # plain device copy used to scale the PMC byte counters
-# Kernel-name fragments of the dominant kernels in rocprofv3 counter files.
-KERNEL_KEYS = {"w13": "gemv_kernel<0,", "w2": "gemv_kernel<1,"}
+# Kernel-name fragments of the dominant kernels in rocprofv3 counter files,
+# per stage and path (dequant-GEMV for few pairs per expert, MFMA tiles else).
+KERNEL_KEYS = {("w13", "gemv"): "gemv_kernel<0,", ("w2", "gemv"): "gemv_kernel<1,",
+               ("w13", "mfma"): "mfma_kernel<0,", ("w2", "mfma"): "mfma_kernel<1,"}
 
 
 def log(*a):
@@ -345,6 +347,52 @@ def traffic_from_pmc(pmc_dirs, kernel_key):
     return int(total), detail
 
 
+def mfma_pair_share(wl):
+    """Fraction of the (token, expert) pairs of set 0 that the call's dispatch
+    sends to the MFMA kernels (the rest run on the dequant-GEMV kernels)."""
+    import torch
+
+    shape, M = wl.shape, wl.cfg.M
+    if wl.tuning is not None:
+        t = wl.tuning
+        only_max_m, max_tokens = t.gemv_only_max_m, t.gemv_max_tokens
+    else:
+        t = wl.pkg._lib.default_tuning(M, shape.topk, shape.E, shape.N, shape.K, shape.group)
+        only_max_m, max_tokens = t.gemv_only_max_m, t.gemv_max_tokens
+    if M <= only_max_m:
+        return 0.0
+    ids = wl.sets[0][2].reshape(-1).long()
+    counts = torch.bincount(ids[(ids >= 0) & (ids < shape.E)], minlength=shape.E)
+    total = int(counts.sum())
+    return float(counts[counts > max_tokens].sum()) / total if total else 0.0
+
+
+def stage_roofline(wl, stage, us):
+    """Roofline of one stage kernel at its average duration `us` (microseconds).
+
+    The bound is the roof that gives the longer minimum time: HBM (8 TB/s)
+    over the touched experts' packed weight + scale bytes, or dense bf16 MFMA
+    (2.5 PFLOP/s) over 2 * pairs * (rows x reduction length) FLOPs.
+    """
+    shape, M = wl.shape, wl.cfg.M
+    nbytes = sum(getattr(wl, f"{stage}_bytes")) / len(wl.sets)
+    rows_k = 2 * shape.N * shape.K if stage == "w13" else shape.K * shape.N
+    flops = 2 * M * shape.topk * rows_k
+    path = "mfma" if mfma_pair_share(wl) >= 0.5 else "gemv"
+    sec = us * 1e-6
+    hbm_bound = nbytes / (HBM_PEAK_GBS * 1e9) >= flops / (BF16_PEAK_TFLOPS * 1e12)
+    kernel = (f"{stage} dequant-GEMV (gemv_kernel)" if path == "gemv"
+              else f"{stage} dequant-MFMA tiles (mfma_kernel)")
+    if hbm_bound:
+        achieved, peak, unit = nbytes / sec / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = flops / sec / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+    return {"bound": "hbm" if hbm_bound else "mfma", "kernel": kernel, "path": path,
+            "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "algorithmic_bytes_per_launch": int(nbytes),
+            "algorithmic_flops_per_launch": int(flops)}
+
+
 def traffic_from_profile(kernel, config_index):
     """The HBM bytes per launch recorded in profiles/ for this kernel/config."""
     import re
@@ -410,27 +458,16 @@ def main(argv=None) -> int:
     log(f"headline: {json.dumps(head)}")
 
     dominant = "w13" if stages["w13"] >= stages["w2"] else "w2"
-    dom_bytes = sum(getattr(wl, f"{dominant}_bytes")) / len(wl.sets)
-    achieved = dom_bytes / (stages[dominant] * 1e-3) / 1e9
+    roofline = stage_roofline(wl, dominant, stages[dominant] * 1e3)
     traffic, traffic_src = None, None
     if args.pmc_dir:
-        traffic, detail = traffic_from_pmc(args.pmc_dir, KERNEL_KEYS[dominant])
+        key = KERNEL_KEYS[(dominant, roofline["path"])]
+        traffic, detail = traffic_from_pmc(args.pmc_dir, key)
         traffic_src = {"pmc": detail}
     else:
-        traffic, path = traffic_from_profile(dominant, head_cfg.index)
-        traffic_src = path
-    roofline = {
-        "bound": "hbm",
-        "kernel": f"{dominant} dequant-GEMV (gemv_kernel)",
-        "achieved": round(achieved, 2),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": traffic,
-        "traffic_source": traffic_src,
-        "avg_launch_us": round(stages[dominant] * 1e3, 3),
-        "algorithmic_bytes_per_launch": int(dom_bytes),
-    }
+        traffic, traffic_src = traffic_from_profile(dominant, head_cfg.index)
+    roofline.update({"traffic": traffic, "traffic_source": traffic_src,
+                     "avg_launch_us": round(stages[dominant] * 1e3, 3)})
 
     sweep = []
     if not args.no_sweep:

@@ -4,44 +4,41 @@
 // and _w4a16_moe_w2_kernel (:502-634): per 16-token block x 64-column tile,
 // tl.dot of bf16 activations with bf16(dequantized weights), fp32 accumulate.
 //
-// Here one workgroup (4 waves, one per SIMD) owns a tile of one expert: up to
-// 256 of its sorted (token, slot) pairs x 256 weight rows.  The align kernel
-// cuts an expert into as few such tiles as possible, so every weight is
-// dequantized once per 256 pairs, and the dequantization work per MFMA falls
-// as the expert's pair count grows.
+// Here one workgroup (8 waves, two per SIMD) owns one tile of one expert --
+// up to 192 of its sorted (token, slot) pairs -- and one or more row tiles of
+// 256 weight rows, run in turn.  The align kernel cuts an expert into as few
+// such tiles as possible (one when it has at most 192 pairs), so every weight
+// is dequantized once per expert at the prefill sizes and the dequantization
+// work per MFMA falls as the expert's pair count grows.
 //
-//   * Each wave owns 64 weight rows (two 32-row MFMA blocks) and reads them
-//     straight from HBM into registers: lane (j, q) of the wave loads the
-//     16-byte group 2t+q of row j for double step t (64 elements of the
-//     reduction axis), four double steps ahead.
+//   * Every global load of the main loop is an LDS DMA (global_load_lds):
+//     the gathered activation rows of a double step (64 elements, 128 bytes
+//     per row), each wave's packed weights (32 rows x 32 bytes) and its
+//     scales, three double steps ahead, so no vector register waits on
+//     memory.  The waits are explicit vector-memory counts.
 //   * A packed word becomes 8 bf16 weights bf16((c - 8) * s) with 17 VALU
 //     instructions: two nibbles at a time are or-ed into fp16 numbers 1024 + c
 //     (bits 0-3) or 1024 + 16 c (bits 4-7), and v_fma_mix_f32 turns each into
 //     (c - 8) * s exactly, (1024 + c) * s - 1032 s or (1024 + 16 c) * (s / 16)
 //     - 72 s; one v_cvt_pk_bf16_f32 rounds two of them.  The product before
 //     the rounding is exact, so the bf16 weight is the reference's.
-//   * The gathered activation rows of one double step (128 bytes per row) go
-//     through a double-buffered LDS tile, loaded into registers two double
-//     steps ahead.
 //   * MFMA v_mfma_f32_32x32x16_bf16 with the weights as the A operand and the
 //     activations as B: the accumulator of a lane holds one token slot and 16
 //     output rows in runs of 4, so the epilogue stores 4 neighbouring outputs
-//     at a time.
-//   * The accumulators (2 x 8 blocks of 16 fp32) live in the accumulation
-//     registers; one wave per SIMD.
+//     at a time.  A wave owns one 32-row block and up to 6 token blocks of 32
+//     (6 x 16 fp32 accumulators).
 //
-// w13 (MODE 0): wave w owns gate rows 32w.. of the tile's 128 gate columns
-// and the matching up rows, so each lane holds gate and up of the same output
-// and the epilogue writes bf16(SiLU(gate) * up) -- the reference's rounding
-// point.
+// w13 (MODE 0): each wave's 32 rows are 16 gate rows and the matching 16 up
+// rows, so each lane holds gate and up of the same output and the epilogue
+// writes bf16(SiLU(gate) * up) -- the reference's rounding point.
 // w2 (MODE 1): the epilogue multiplies by the routing weight and writes the
 // partial row of the (token, slot) pair, rounded to bf16 like the reference's
 // partial buffer (kernels/w4a16_moe.py:311) unless the call keeps fp32
 // partials (M <= 4, where the reference accumulates in fp32).
 //
-// Workgroup ids are remapped so that the row tiles of one token tile run on
-// one XCD (consecutive hardware ids round-robin over the 8 XCDs) and share
-// its L2 for the gathered activation rows.
+// Workgroup ids are remapped so that the work items of one tile run on one
+// XCD (consecutive hardware ids round-robin over the 8 XCDs) and share its L2
+// for the gathered activation rows.
 #include <type_traits>
 
 #include "common.hpp"
