@@ -39,7 +39,7 @@ struct Tuning {
   int gemv_only_max_m;  // M at or below this: every expert on the GEMV kernels
   int gemv_max_tokens;  // above it: experts with more pairs go to MFMA tiles
   int tc;               // GEMV token rows per pass (0 = launcher's choice)
-  int tile_m;           // MFMA tile height
+  int tile_m;           // MFMA tile height (0 = built-in, see compute_layout)
   int upw;              // GEMV row slabs per workgroup (0 = launcher's choice)
   int lpr;              // GEMV lanes per weight row (0 = launcher's choice)
   int w2_fused_max_m;   // M at or below this: w2 and the top-k sum as one kernel
@@ -119,6 +119,10 @@ int pick_row_tiles(int64_t n_tiles_n, int64_t steps, int64_t n_tok, int64_t E,
 // Average (token, slot) pairs per expert from which the built-in split sends
 // every expert to the MFMA kernels (gemv_max_tokens 0, no GEMV launches).
 constexpr int64_t kAllMfmaMinPairs = 32;
+// Average pairs per expert below which the built-in MFMA tile is 128 slots.
+// Measured on MI355X (E=256, top-10): M=256 skewed 307 vs 406 us, M=1024
+// 505 vs 552 us; at M=4096 192 wins (1049 vs 1171 us uniform).
+constexpr int64_t kTile128MaxPairs = 64;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -131,7 +135,7 @@ int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
 }
 
 Tuning default_tuning() {
-  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, kMfmaTileM, 0, 0, kW2FusedMaxM, true, 0};
+  return Tuning{kGemvOnlyMaxM, kGemvMaxTokens, 0, 0, 0, 0, kW2FusedMaxM, true, 0};
 }
 
 // NULL selects the built-in choices.
@@ -191,7 +195,11 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   L->upw = T.upw;
   L->lpr = T.lpr;
   const int64_t heavy = std::min<int64_t>(E, (int64_t)n_tok / (T.gemv_max_tokens + 1));
-  L->tile_m = T.tile_m;
+  // Built-in tile height: 128 slots while experts average fewer than 64
+  // pairs (more, shorter tiles: an expert's long tile is the tail of the
+  // launch under skewed routing), 192 from there.
+  L->tile_m = T.tile_m ? T.tile_m
+                       : ((int64_t)n_tok < kTile128MaxPairs * E ? kMfmaTileMMin : kMfmaTileMMax);
   L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
                         : std::min<int64_t>((int64_t)n_tok, L->nb);
@@ -479,7 +487,7 @@ int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts, int64
   tuning->gemv_only_max_m = T.gemv_only_max_m;
   tuning->gemv_max_tokens = L.gemv_max_tokens;
   tuning->gemv_tokens_per_pass = T.tc;
-  tuning->mfma_tile_m = T.tile_m;
+  tuning->mfma_tile_m = L.tile_m;
   tuning->gemv_units_per_wg = T.upw;
   tuning->gemv_lanes_per_row = T.lpr;
   tuning->w2_fused_max_m = T.w2_fused_max_m;

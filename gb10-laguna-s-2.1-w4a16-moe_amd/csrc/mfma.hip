@@ -63,6 +63,13 @@ constexpr int kAbufs = 4;                    // activation buffers (double steps
 constexpr int kXcds = 8;
 constexpr int kStepK = 64;                   // reduction elements per double step
 constexpr int kUnroll = 4;                   // double steps per loop iteration
+// MFMAs of a double step's last k-step issued before the end-of-step wait and
+// barrier (the rest follow the next step's operand reads); -1: half of them.
+// Overridable at build time for tuning sweeps.
+#ifndef W4A16_MFMA_KSPLIT
+#define W4A16_MFMA_KSPLIT -1
+#endif
+constexpr int kMfmaSplit = W4A16_MFMA_KSPLIT;
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
@@ -509,7 +516,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       // barrier, then step t+1's operand reads (into af[0], af[1]) behind the
       // remaining MFMAs.
       __builtin_amdgcn_sched_barrier(0);
-      constexpr int kSplit = (MC + 1) / 2;
+      constexpr int kSplit = kMfmaSplit < 0 ? (MC + 1) / 2 : (kMfmaSplit > MC ? MC : kMfmaSplit);
       mfmas(3, 0, kSplit);
       __builtin_amdgcn_sched_barrier(0);
       // Step t+1's data: behind its weight DMA (step t-2) are step t-1's

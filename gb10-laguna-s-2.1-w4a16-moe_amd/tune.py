@@ -64,14 +64,18 @@ def effective(M: int, N: int, K: int, t) -> tuple:
         fused = M <= (t.w2_fused_max_m or 4)
         return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg, t.gemv_lanes_per_row,
                 fused)
-    return ("split", t.gemv_max_tokens, t.gemv_tokens_per_pass, t.gemv_units_per_wg,
-            t.gemv_lanes_per_row)
+    return ("split", t.gemv_max_tokens,
+            t.gemv_tokens_per_pass if t.gemv_max_tokens else 0,
+            t.gemv_units_per_wg if t.gemv_max_tokens else 0,
+            t.gemv_lanes_per_row if t.gemv_max_tokens else 0,
+            t.mfma_tile_m or 192, t.mfma_row_tiles)
 
 
-def candidates(M: int, N: int, K: int, Tuning, always: int):
+def candidates(M: int, N: int, K: int, Tuning, always: int, base=None):
     """Every distinct dispatch choice worth timing at M, the built-in one
-    first (slow candidates are pruned against it)."""
-    out = [Tuning()]
+    (`base`, the library's own choice for M) first; slow candidates are pruned
+    against it."""
+    out = [base if base is not None else Tuning()]
     for tc in (0, 1, 2, 4):
         if tc == 1 and M > 4:
             continue
@@ -85,6 +89,8 @@ def candidates(M: int, N: int, K: int, Tuning, always: int):
             for tc in (0, 2, 4):
                 out.append(Tuning(0, thr, tc, 0))
         out += [Tuning(0, 4, 0, 0, upw) for upw in (1, 2, 4)]
+        # MFMA token tiles of at most 128 slots (more, smaller tiles)
+        out += [Tuning(0, thr, 0, 128) for thr in (0, 4)]
     seen, uniq = set(), []
     for t in out:
         key = effective(M, N, K, t)
@@ -176,13 +182,14 @@ def tune(ms, E, N, K, group, topk, seed=0, check_tol=5e-3):
         benches = {"uniform": _Bench(pkg, shape, weights, M, dev, seed_base=1000 * M),
                    "skewed": _Bench(pkg, shape, weights, M, dev, seed_base=1000 * M,
                                     skewed=True)}
-        base = T.Tuning()  # the built-in choices
+        # the built-in choices for M, as explicit values
+        base = T.Tuning.from_struct(pkg._lib.default_tuning(M, topk, E, N, K, group))
         refs = {k: b.call(0, base).float() for k, b in benches.items()}
         base_us = {k: b.graph_us(base) for k, b in benches.items()}
         base_q = {k: b.quick_us(base) for k, b in benches.items()}
         rows = []
         best = (2.0, base, dict(base_us))
-        for cand in candidates(M, N, K, T.Tuning, T.ALWAYS)[1:]:
+        for cand in candidates(M, N, K, T.Tuning, T.ALWAYS, base)[1:]:
             for k, b in benches.items():
                 out = b.call(0, cand).float()
                 torch.cuda.synchronize()
@@ -197,6 +204,7 @@ def tune(ms, E, N, K, group, topk, seed=0, check_tol=5e-3):
                 continue
             us = {k: b.graph_us(cand) for k, b in benches.items()}
             score = sum(us[k] / base_us[k] for k in us)
+            log(f"  M={M} {cand}: score {score:.3f}")
             rows.append({"tuning": cand.to_dict(), "score": round(score, 4),
                          "us": {k: round(v, 3) for k, v in us.items()}})
             if score < best[0]:
@@ -239,6 +247,8 @@ def main(argv=None) -> int:
     ap.add_argument("--topk", type=int, default=10)
     ap.add_argument("--out", default=None, help="directory for the table JSON")
     ap.add_argument("--report", default=None, help="write every candidate's time here")
+    ap.add_argument("--replace", action="store_true",
+                    help="write only the tuned M (default: merge into an existing table)")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         log("tune.py needs the GPU the table is for")
@@ -254,6 +264,10 @@ def main(argv=None) -> int:
     out_dir = Path(args.out) if args.out else T.CONFIG_DIR
     out_dir.mkdir(parents=True, exist_ok=True)
     path = out_dir / T.config_name(args.E, args.N, args.K, args.group, T.device_name())
+    if path.exists() and not args.replace:
+        # keep the entries of an existing table for the M not tuned now
+        old = T.load_table(args.E, args.N, args.K, args.group, T.device_name(), out_dir) or {}
+        table = {**{m: t for m, t in old.items() if m not in table}, **table}
     path.write_text(T.dump_table(table))
     log(f"wrote {path}")
     if args.report:

@@ -53,6 +53,10 @@ class Tuning:
         return t
 
     @classmethod
+    def from_struct(cls, t: _lib.TuningStruct) -> "Tuning":
+        return cls(**{k: int(getattr(t, k)) for k in cls.__dataclass_fields__})
+
+    @classmethod
     def from_dict(cls, d: dict) -> "Tuning":
         unknown = set(d) - set(cls.__dataclass_fields__)
         if unknown:

@@ -45,8 +45,13 @@ def test_default_tuning_and_workspace_sizes(pkg):
     d = L.default_tuning(16, 10, 256, 1024, 3072, 32)
     assert (d.gemv_only_max_m, d.gemv_max_tokens, d.gemv_tokens_per_pass, d.mfma_tile_m,
             d.gemv_units_per_wg, d.gemv_lanes_per_row, d.w2_fused_max_m) == \
-        (24, 4, 0, 192, 0, 0, 4)
+        (24, 4, 0, 128, 0, 0, 4)
     assert d.mfma_row_tiles == 0
+    # built-in MFMA tile height: 128 slots below 64 pairs per expert, then 192
+    assert L.default_tuning(1024, 10, 256, 1024, 3072, 32).mfma_tile_m == 128
+    assert L.default_tuning(1638, 10, 256, 1024, 3072, 32).mfma_tile_m == 128
+    assert L.default_tuning(1639, 10, 256, 1024, 3072, 32).mfma_tile_m == 192
+    assert L.default_tuning(4096, 10, 256, 1024, 3072, 32).mfma_tile_m == 192
     for M in (1, 16, 64, 4096):
         base = L.workspace_size(M, 10, 256, 1024, 3072, 32)
         assert L.workspace_size_ex(M, 10, 256, 1024, 3072, 32, None) == base
@@ -103,6 +108,22 @@ def _valid(pkg, t):
 
 def _tune_module(pkg):
     return importlib.import_module(pkg.__name__ + ".tune")
+
+
+def test_builtin_as_explicit_tuning(pkg):
+    """Tuning.from_struct of the library's built-in choice for M reproduces it:
+    the same workspace, and the all-MFMA split from 32 pairs per expert."""
+    L = pkg._lib
+    for M in (1, 16, 64, 1024, 4096):
+        t = pkg.Tuning.from_struct(L.default_tuning(M, 10, 256, 1024, 3072, 32))
+        assert t.to_struct().gemv_max_tokens == t.gemv_max_tokens
+        assert L.workspace_size_ex(M, 10, 256, 1024, 3072, 32, t.to_struct()) == \
+            L.workspace_size(M, 10, 256, 1024, 3072, 32)
+        assert (t.gemv_max_tokens == 0) == (M * 10 >= 32 * 256)
+    tune = _tune_module(pkg)
+    base = pkg.Tuning.from_struct(L.default_tuning(4096, 10, 256, 1024, 3072, 32))
+    cands = tune.candidates(4096, 1024, 3072, pkg.Tuning, pkg.tuning.ALWAYS, base)
+    assert cands[0] == base and any(c.mfma_tile_m == 128 for c in cands)
 
 
 def test_candidates_are_valid(pkg):
