@@ -25,40 +25,136 @@
 namespace w4a16 {
 namespace {
 
-// Exclusive scan of one int per thread over the workgroup.
-__device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
+// Inclusive scan over the 64 lanes of a wave with DPP lane moves (no LDS):
+// shifts by 1, 2, 4 and 8 lanes inside each row of 16 (lanes without a source
+// add 0), then the last lane of row 0 is added to row 1 and of row 2 to row 3
+// (row_bcast:15), then the last lane of row 1 to rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+
+// NV exclusive scans of one int per thread over the workgroup at once (three
+// barriers); wt is LDS of NV x 17 ints.  All threads must call.
+template <int NV>
+__device__ void block_exclusive_scan_n(const int (&v)[NV], int (&excl)[NV], int (&total)[NV],
+                                       int* wt) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  int x = v;
+  int x[NV];
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
+  for (int k = 0; k < NV; ++k) {
+    x[k] = wave_inclusive_scan(v[k]);
+    if (lane == 63) wt[k * 17 + wid] = x[k];
   }
-  if (lane == 63) wave_tot[wid] = x;
   __syncthreads();
   if (wid == 0) {
-    const int t = lane < nw ? wave_tot[lane] : 0;
-    int s = t;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int y = __shfl_up(s, d, 64);
-      if (lane >= d) s += y;
+    for (int k = 0; k < NV; ++k) {
+      const int t = lane < nw ? wt[k * 17 + lane] : 0;
+      const int sc = wave_inclusive_scan(t);
+      if (lane < nw) wt[k * 17 + lane] = sc - t;
+      if (lane == nw - 1) wt[k * 17 + 16] = sc;
     }
-    if (lane < nw) wave_tot[lane] = s - t;
-    if (lane == nw - 1) wave_tot[16] = s;
   }
   __syncthreads();
-  *total = wave_tot[16];
-  const int excl = x - v + wave_tot[wid];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    total[k] = wt[k * 17 + 16];
+    excl[k] = x[k] - v[k] + wt[k * 17 + wid];
+  }
   __syncthreads();
-  return excl;
+}
+
+// Exclusive scan of one int per thread over the workgroup; wave_tot is LDS
+// of 17 ints.  All threads must call.
+__device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
+  const int vv[1] = {v};
+  int ex[1], tt[1];
+  block_exclusive_scan_n<1>(vv, ex, tt, wave_tot);
+  *total = tt[0];
+  return ex[0];
+}
+
+// Token blocks (32 slots) of the tallest MFMA tile: the tile list is ordered
+// by height class, tallest first.
+constexpr int kTileClasses = kMfmaTileMMax / 32;
+
+// Work lists of the fused call.  An expert with more than gemv_max_tokens
+// pairs gets ceil(count / tile_m) MFMA tiles of near-equal size (multiples of
+// 32 slots but the last); the tiles are listed by height class, tallest
+// first (experts ascending within a class), so that the MFMA launch starts
+// its longest tiles first.  Every other routed expert's single sorted block
+// goes to the GEMV list.  Thread tid owns experts e0 .. e0 + ipt - 1; wt is
+// LDS of (kTileClasses + 1) x 17 ints.  All threads must call.
+__device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const int32_t* off,
+                                 int e0, int ipt, int* wt) {
+  constexpr int NC = kTileClasses;
+  const int E = a.num_experts, B = a.block, thr = a.gemv_max_tokens;
+  // class of a tile of n slots: NC - (token blocks)
+  auto cls = [](int n) { return NC - ((n + 31) >> 5); };
+  int v[NC + 1];  // tiles per class, then GEMV blocks
+#pragma unroll
+  for (int k = 0; k <= NC; ++k) v[k] = 0;
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e >= E) break;
+    const int c = tot[e];
+    if (c > thr) {
+      const int n_ch = (c + a.tile_m - 1) / a.tile_m;
+      const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
+      const int n_t = (c + per - 1) / per;
+      const int kf = cls(per), kl = cls(c - (n_t - 1) * per);
+#pragma unroll
+      for (int k = 0; k < NC; ++k) v[k] += (k == kf ? n_t - 1 : 0) + (k == kl ? 1 : 0);
+    } else if (c > 0) {
+      ++v[NC];
+    }
+  }
+  int pos[NC + 1], total[NC + 1];
+  block_exclusive_scan_n<NC + 1>(v, pos, total, wt);
+  int n_tiles = 0;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    pos[k] += n_tiles;
+    n_tiles += total[k];
+  }
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e >= E) break;
+    const int c = tot[e];
+    if (c > thr) {
+      const int n_ch = (c + a.tile_m - 1) / a.tile_m;
+      const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;
+      for (int s0 = 0; s0 < c; s0 += per) {
+        const int n = min(per, c - s0);
+        const int k = cls(n);
+        int p = 0;
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+          if (j == k) p = pos[j]++;
+        a.tiles[p] = make_int4(e, off[e] + s0, n, 0);
+      }
+    } else if (c > 0) {
+      a.gemv_blocks[pos[NC]++] = off[e] / B;
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.n_tiles[0] = n_tiles;
+    a.n_gemv[0] = total[NC];
+  }
 }
 
 __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   extern __shared__ int32_t smem[];
   __shared__ int32_t wave_tot[17];
+  __shared__ int32_t wl_tot[(kTileClasses + 1) * 17];
   __shared__ int32_t s_drop;
 
   const int nthr = blockDim.x;
@@ -148,40 +244,8 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   if (tid == 0) off[E] = total;
   __syncthreads();
 
-  // 3b. work lists of the fused call: MFMA tiles for heavy experts, the
-  // single block of every light expert for the GEMV path.
-  if (a.tiles) {
-    const int thr = a.gemv_max_tokens;
-    int nt_local = 0, ng_local = 0;
-    for (int i = 0; i < ipt; ++i) {
-      const int e = e0 + i;
-      if (e < E) {
-        const int c = tot[e];
-        nt_local += c > thr ? (c + a.tile_m - 1) / a.tile_m : 0;
-        ng_local += (c > 0 && c <= thr) ? 1 : 0;
-      }
-    }
-    int n_tiles = 0, n_gemv = 0;
-    int tbase = block_exclusive_scan(nt_local, wave_tot, &n_tiles);
-    int gbase = block_exclusive_scan(ng_local, wave_tot, &n_gemv);
-    for (int i = 0; i < ipt; ++i) {
-      const int e = e0 + i;
-      if (e >= E) continue;
-      const int c = tot[e];
-      if (c > thr) {
-        const int n_ch = (c + a.tile_m - 1) / a.tile_m;
-        const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
-        for (int s0 = 0; s0 < c; s0 += per)
-          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(per, c - s0), 0);
-      } else if (c > 0) {
-        a.gemv_blocks[gbase++] = off[e] / B;
-      }
-    }
-    if (tid == 0) {
-      a.n_tiles[0] = n_tiles;
-      a.n_gemv[0] = n_gemv;
-    }
-  }
+  // 3b. work lists of the fused call
+  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, wl_tot);
 
   for (int i = tid; i < nw * E; i += nthr) cnt[i] += off[i % E];
   __syncthreads();
@@ -294,6 +358,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
                                                              const int32_t* cdrop) {
   extern __shared__ int32_t smem[];
   __shared__ int32_t wave_tot[17];
+  __shared__ int32_t wl_tot[(kTileClasses + 1) * 17];
   constexpr int nw = kChunkWaves;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -384,38 +449,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   if (g != 0) return;
 
   // 6. workgroup 0: work lists, sentinels, block experts, scalars
-  if (a.tiles) {
-    const int thr = a.gemv_max_tokens;
-    int nt_local = 0, ng_local = 0;
-    for (int i = 0; i < ipt; ++i) {
-      const int e = e0 + i;
-      if (e < E) {
-        const int c = tot[e];
-        nt_local += c > thr ? (c + a.tile_m - 1) / a.tile_m : 0;
-        ng_local += (c > 0 && c <= thr) ? 1 : 0;
-      }
-    }
-    int n_tiles = 0, n_gemv = 0;
-    int tbase = block_exclusive_scan(nt_local, wave_tot, &n_tiles);
-    int gbase = block_exclusive_scan(ng_local, wave_tot, &n_gemv);
-    for (int i = 0; i < ipt; ++i) {
-      const int e = e0 + i;
-      if (e >= E) continue;
-      const int c = tot[e];
-      if (c > thr) {
-        const int n_ch = (c + a.tile_m - 1) / a.tile_m;
-        const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
-        for (int s0 = 0; s0 < c; s0 += per)
-          a.tiles[tbase++] = make_int4(e, off[e] + s0, min(per, c - s0), 0);
-      } else if (c > 0) {
-        a.gemv_blocks[gbase++] = off[e] / B;
-      }
-    }
-    if (tid == 0) {
-      a.n_tiles[0] = n_tiles;
-      a.n_gemv[0] = n_gemv;
-    }
-  }
+  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, wl_tot);
   for (int e = tid; e < E; e += kChunk) {
     const int p1 = off[e + 1];
     for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;

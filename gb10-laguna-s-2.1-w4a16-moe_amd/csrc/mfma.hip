@@ -36,9 +36,9 @@
 // partial buffer (kernels/w4a16_moe.py:311) unless the call keeps fp32
 // partials (M <= 4, where the reference accumulates in fp32).
 //
-// Workgroup ids are remapped so that the work items of one tile run on one
-// XCD (consecutive hardware ids round-robin over the 8 XCDs) and share its L2
-// for the gathered activation rows.
+// Workgroup ids are mapped so that the work items of one tile run on one XCD
+// (consecutive hardware ids round-robin over the 8 XCDs) and share its L2 for
+// the gathered activation rows, and each XCD runs its tallest tiles first.
 #include <type_traits>
 
 #include "common.hpp"
@@ -96,12 +96,6 @@ __device__ __forceinline__ float fma_half(uint32_t h2, int hi, float s, float b)
 // that follows.
 __device__ __forceinline__ float silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-}
-
-__device__ __forceinline__ int xcd_remap(int bid, int n) {
-  const int per = n / kXcds;
-  if (bid >= per * kXcds) return bid;
-  return (bid % kXcds) * per + bid / kXcds;
 }
 
 // s_waitcnt with only the vector-memory count: wait until at most n vector
@@ -560,14 +554,18 @@ void mfma_kernel(const MfmaLaunch a) {
   // A work item is up to row_tiles consecutive row tiles of one token tile.
   const int per_item = a.row_tiles;
   const int items_per_tile = (n_tiles_n + per_item - 1) / per_item;
-  // The grid is sized for the most tiles a routing can produce; the align
-  // kernel wrote the real count.  Workgroups past it leave at once, and the
-  // XCD remap runs over the real ones so that every XCD gets its share.
-  const int n_active = a.header[2] * items_per_tile;
-  if ((int)blockIdx.x >= n_active) return;
-  const int bid = xcd_remap(blockIdx.x, n_active);
-  const int tile = bid / items_per_tile;
-  const int nt0 = (bid - tile * items_per_tile) * per_item;
+  // Tiles are dealt over the 8 XCDs (consecutive workgroup ids go to
+  // consecutive XCDs), in rounds of 8 that alternate direction, and the work
+  // items of one tile run back to back on its XCD, sharing its L2 for the
+  // gathered activation rows.  The align kernel lists the tiles tallest
+  // first, so every XCD starts its longest tiles first and hands out the
+  // rest as its CUs free up.  The grid is sized for the most tiles a routing
+  // can produce; workgroups past the real count (header[2]) leave at once.
+  const int xcd = (int)blockIdx.x % kXcds, slot = (int)blockIdx.x / kXcds;
+  const int round = slot / items_per_tile;
+  const int tile = kXcds * round + ((round & 1) ? kXcds - 1 - xcd : xcd);
+  if (tile >= a.header[2]) return;
+  const int nt0 = (slot - round * items_per_tile) * per_item;
   const int nrt = min(per_item, n_tiles_n - nt0);
   const int4 info = a.tiles[tile];
   const int e = info.x, start = info.y;
@@ -598,8 +596,8 @@ hipError_t launch_mfma_t(const MfmaLaunch& a, hipStream_t stream) {
   const int64_t act_rows = MODE == 0 ? a.n_tok / a.topk : a.n_tok;
   if (act_rows * a.ld_act * 2 > (int64_t)UINT32_MAX - 4096) return hipErrorInvalidValue;
   if (a.row_tiles < 1) return hipErrorInvalidValue;
-  const int64_t grid =
-      (int64_t)a.max_tiles * ((rows_total / kTN + a.row_tiles - 1) / a.row_tiles);
+  const int64_t grid = (int64_t)(a.max_tiles + kXcds - 1) / kXcds * kXcds *
+                       ((rows_total / kTN + a.row_tiles - 1) / a.row_tiles);
   if (grid <= 0) return hipSuccess;
   const dim3 g((unsigned)grid), b(kWaves * 64);
   switch (a.group) {

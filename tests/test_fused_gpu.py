@@ -169,7 +169,9 @@ def test_intermediate_matches_oracle(pkg, orc, synth, dev):
 def _expected_work_lists(counts, offs, thr, tile_m):
     """MFMA tiles and GEMV blocks the align kernel writes: an expert with more
     than thr pairs gets ceil(c / tile_m) tiles of near-equal size (multiples
-    of 32 slots but the last), every other routed expert its one block."""
+    of 32 slots but the last), listed tallest first (in 32-slot blocks;
+    experts ascending within a height); every other routed expert its one
+    block."""
     tiles, gemv = [], []
     for e, c in enumerate(int(c) for c in counts):
         if c > thr:
@@ -178,6 +180,7 @@ def _expected_work_lists(counts, offs, thr, tile_m):
             tiles += [(e, int(offs[e]) + s0, min(per, c - s0)) for s0 in range(0, c, per)]
         elif c > 0:
             gemv.append(int(offs[e]) // 16)
+    tiles.sort(key=lambda t: -((t[2] + 31) // 32))  # stable: expert order within a height
     return tiles, gemv
 
 
