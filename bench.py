@@ -312,6 +312,31 @@ def calibration_copy(dev):
     del a, b
 
 
+def measured_copy_bw(dev, nbytes=1 << 30, reps=5):
+    """A plain device-to-device copy of nbytes, best of reps: (read + written
+    bytes) / time, the measured HBM figure reported beside the 8 TB/s peak."""
+    import torch
+
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    a.fill_(1)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        b.copy_(a)
+        en.record()
+        torch.cuda.synchronize()
+        best = min(best, st.elapsed_time(en) * 1e-3)
+    del a, b
+    torch.cuda.empty_cache()
+    return {"GB_s": round(2 * nbytes / best / 1e9, 1), "bytes_copied": nbytes,
+            "note": "torch device-to-device copy, (read + written bytes) / time, best of "
+                    f"{reps}"}
+
+
 def traffic_from_pmc(pmc_dirs, kernel_key):
     """HBM bytes per launch of a kernel from rocprofv3 --pmc CSV output.
 
@@ -486,6 +511,8 @@ def main(argv=None) -> int:
             del w
             torch.cuda.empty_cache()
 
+    copy_bw = measured_copy_bw(dev)
+    log(f"measured device copy: {copy_bw['GB_s']} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
@@ -517,6 +544,7 @@ def main(argv=None) -> int:
                    "parallelism": "single GPU"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline,
+        "hbm_copy_measured": copy_bw,
         "cpu_baseline": cpu,
         "configs": sweep,
     }
