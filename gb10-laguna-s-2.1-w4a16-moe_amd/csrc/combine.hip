@@ -14,65 +14,96 @@
 namespace w4a16 {
 namespace {
 
-// Four consecutive partial values of row `row` starting at element 4*k4.
-template <bool BF16>
-__device__ __forceinline__ float4 load4(const void* partial, int64_t row, int K, int k4) {
-  if constexpr (BF16) {
-    const uint2 v = reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(partial) +
-                                                   row * K)[k4];
-    return make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16),
-                       bf16_to_f32(v.y & 0xFFFFu), bf16_to_f32(v.y >> 16));
-  } else {
-    return reinterpret_cast<const float4*>(static_cast<const float*>(partial) + row * K)[k4];
-  }
-}
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Slots whose partial loads are in flight together.
+constexpr int kSlotBatch = 16;
+constexpr int kCombineThreads = 128;
+
+// One thread owns VPT consecutive outputs of one token (8 for bf16 partials,
+// 4 for fp32: one 16-byte load per slot).  The ids of a batch of slots are
+// read with every slot's partial row (a slot with an id outside [0, E) has an
+// unwritten row: it is read and left out), all in flight together, and the
+// values are added in slot order from +0.0 -- the order of the reference's
+// sum, so the result does not depend on the batching.
 template <bool VEC_STORE, bool BF16>
-__global__ __launch_bounds__(256) void combine_kernel(const CombineLaunch a) {
-  const int kchunks = (a.K / 4 + 255) / 256;
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineLaunch a) {
+  constexpr int VPT = BF16 ? 8 : 4;
+  const int per_row = a.K / VPT;
+  const int kchunks = (per_row + kCombineThreads - 1) / kCombineThreads;
   const int m = blockIdx.x / kchunks;
-  const int k4 = (blockIdx.x - m * kchunks) * 256 + threadIdx.x;  // 4 outputs
-  if (k4 * 4 >= a.K) return;
+  const int c = (blockIdx.x - m * kchunks) * kCombineThreads + threadIdx.x;
+  if (c >= per_row) return;
   const int64_t row0 = (int64_t)m * a.topk;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int t = 0; t < a.topk; ++t) {
-    const int e = a.ids[row0 + t];
-    if (e >= 0 && e < a.num_experts) {
-      const float4 v = load4<BF16>(a.partial, row0 + t, a.K, k4);
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
+  const size_t row_bytes = (size_t)a.K * (BF16 ? 2 : 4);
+  const char* base = static_cast<const char*>(a.partial) + (size_t)c * 16;
+  float acc[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) acc[i] = 0.0f;
+  for (int t0 = 0; t0 < a.topk; t0 += kSlotBatch) {
+    const int nb = min(kSlotBatch, a.topk - t0);
+    bool ok[kSlotBatch];
+    u32x4_t v[kSlotBatch];
+#pragma unroll
+    for (int j = 0; j < kSlotBatch; ++j) {
+      ok[j] = false;
+      v[j] = u32x4_t{0u, 0u, 0u, 0u};
+      if (j < nb) {  // uniform
+        const int e = a.ids[row0 + t0 + j];
+        ok[j] = e >= 0 && e < a.num_experts;
+        v[j] = *reinterpret_cast<const u32x4_t*>(base + (size_t)(row0 + t0 + j) * row_bytes);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kSlotBatch; ++j) {
+      if (!ok[j]) continue;
+      if constexpr (BF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += bf16_to_f32(v[j][i] & 0xFFFFu);
+          acc[2 * i + 1] += bf16_to_f32(v[j][i] >> 16);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += __uint_as_float(v[j][i]);
+      }
     }
   }
-  uint16_t* o = a.out + (int64_t)m * a.ld_out + 4 * k4;
-  const uint32_t b0 = f32_to_bf16(acc.x), b1 = f32_to_bf16(acc.y);
-  const uint32_t b2 = f32_to_bf16(acc.z), b3 = f32_to_bf16(acc.w);
+  uint16_t* o = a.out + (int64_t)m * a.ld_out + (int64_t)c * VPT;
+  uint32_t b[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) b[i] = f32_to_bf16(acc[i]);
   if (VEC_STORE) {
-    *reinterpret_cast<uint2*>(o) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+    if constexpr (VPT == 8)
+      *reinterpret_cast<u32x4_t*>(o) =
+          u32x4_t{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+    else
+      *reinterpret_cast<uint2*>(o) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
   } else {
-    o[0] = (uint16_t)b0;
-    o[1] = (uint16_t)b1;
-    o[2] = (uint16_t)b2;
-    o[3] = (uint16_t)b3;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) o[i] = (uint16_t)b[i];
   }
 }
 
 template <bool BF16>
 void launch_combine_t(const CombineLaunch& a, dim3 grid, bool vec, hipStream_t stream) {
   if (vec)
-    hipLaunchKernelGGL((combine_kernel<true, BF16>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<true, BF16>), grid, dim3(kCombineThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((combine_kernel<false, BF16>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<false, BF16>), grid, dim3(kCombineThreads), 0, stream, a);
 }
 
 }  // namespace
 
 hipError_t launch_combine(const CombineLaunch& a, hipStream_t stream) {
   if (a.M <= 0) return hipSuccess;
-  const int64_t kchunks = (a.K / 4 + 255) / 256;
+  const int vpt = a.partial_bf16 ? 8 : 4;
+  // 16-byte partial loads: K a multiple of 8 and a 16-byte aligned buffer
+  if (a.K % 8 != 0 || reinterpret_cast<uintptr_t>(a.partial) % 16 != 0)
+    return hipErrorInvalidValue;
+  const int64_t kchunks = (a.K / vpt + kCombineThreads - 1) / kCombineThreads;
   const dim3 grid((unsigned)(kchunks * a.M));
-  const bool vec = (reinterpret_cast<uintptr_t>(a.out) % 8 == 0) && (a.ld_out % 4 == 0);
+  const bool vec = (reinterpret_cast<uintptr_t>(a.out) % (2 * vpt) == 0) && (a.ld_out % vpt == 0);
   if (a.partial_bf16)
     launch_combine_t<true>(a, grid, vec, stream);
   else
