@@ -62,7 +62,7 @@ MALL_BYTES = 256 * 2**20       # Infinity Cache
 # 226.3 GB/s on NVIDIA GB10 (results/showdown2.json:1104; README.md:62-70).
 REFERENCE_GBS_M16 = 226.3
 STAGES = ("align", "w13", "w2", "combine")
-CALIB_BYTES = 512 * 2**20       # plain device copy used to scale the PMC byte counters
+CALIB_BYTES = 2**30            # plain device copy: PMC byte-counter scale and measured copy BW
 # Kernel-name fragments of the dominant kernels in rocprofv3 counter files,
 # per stage and path (dequant-GEMV for few pairs per expert, MFMA tiles else).
 KERNEL_KEYS = {("w13", "gemv"): "gemv_kernel<0,", ("w2", "gemv"): "gemv_kernel<1,",
@@ -312,7 +312,7 @@ def calibration_copy(dev):
     del a, b
 
 
-def measured_copy_bw(dev, nbytes=1 << 30, reps=5):
+def measured_copy_bw(dev, nbytes=CALIB_BYTES, reps=5):
     """A plain device-to-device copy of nbytes, best of reps: (read + written
     bytes) / time, the measured HBM figure reported beside the 8 TB/s peak."""
     import torch
