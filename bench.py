@@ -12,14 +12,17 @@ headline value is BASELINE.json's configs[1]: E=256, top-10, K=3072, N=1024,
 group 32, M=16 tokens, uniform routing.  The other configurations are reported
 in "configs".
 
-Timing: the calls are captured in a HIP graph that cycles through several
-routing/hidden sets (so the touched weights exceed the 256 MB Infinity Cache
-several times over); W warmup calls, then exactly K timed calls bracketed by
-device synchronisation and events on the capturing stream.
+Timing: the K timed calls are captured as one HIP graph (chunks of at most
+2048 calls) that cycles through several routing/hidden sets, so the touched
+weights exceed the 256 MB Infinity Cache several times over and the graph's
+per-replay overhead is spread over all K calls, as in a serving loop that
+captures a whole forward pass; W warmup calls and one untimed replay, then
+exactly K timed calls bracketed by device synchronisation and events on the
+capturing stream.
 
-Per-kernel durations come from replaying graphs of one stage at a time
-(w4a16_moe_run_stage_ex, with the dispatch tuning the call itself uses) over
-the same sets, timed with events on the stream the
+Per-kernel durations come from graphs of one stage at a time
+(w4a16_moe_run_stage_ex, with the dispatch tuning the call itself uses) that
+cycle over the same sets several times, timed with events on the stream the
 kernels run on; the dominant kernel's algorithmic bytes / duration is the
 roofline "achieved" figure.
 
@@ -113,8 +116,12 @@ class Workload:
         for j in range(warmup):
             self.call(j % n)
         torch.cuda.synchronize()
-        full, rem = divmod(steps, n)
-        graphs = []
+        # The timed calls are captured as one graph of exactly `steps` calls
+        # cycling through the sets (chunks of at most kMaxGraph calls), as a
+        # serving loop captures a whole forward pass: the per-replay launch
+        # overhead is then spread over every call, not over one set cycle.
+        kMaxGraph = 2048
+        chunks = [min(kMaxGraph, steps - s0) for s0 in range(0, steps, kMaxGraph)]
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
@@ -122,34 +129,30 @@ class Workload:
                 self.call(i)
         torch.cuda.current_stream().wait_stream(stream)
         torch.cuda.synchronize()
-        g_all = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_all):
-            for i in range(n):
-                self.call(i)
-        graphs.append(g_all)
-        g_rem = None
-        if rem:
-            g_rem = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g_rem):
-                for i in range(rem):
-                    self.call(i)
-        # one untimed replay so first-replay costs stay out of the timed region
-        g_all.replay()
+        graphs = {}
+        for c in sorted(set(chunks)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(c):
+                    self.call(i % n)
+            graphs[c] = g
+        # one untimed pass so first-replay costs stay out of the timed region
+        for c in chunks:
+            graphs[c].replay()
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record()
-        for _ in range(full):
-            g_all.replay()
-        if g_rem is not None:
-            g_rem.replay()
+        for c in chunks:
+            graphs[c].replay()
         end.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = start.elapsed_time(end)
-        nbytes = full * sum(self.bytes) + sum(self.bytes[:rem])
+        nbytes = sum(self.bytes[i % n] for c in chunks for i in range(c))
+        del graphs
         return {"elapsed_ms": ms, "wall_s": wall, "steps": steps, "bytes": nbytes}
 
     # ---- per-stage timing ---------------------------------------------------
@@ -187,19 +190,22 @@ class Workload:
                 for i in range(len(self.sets)):
                     L.check(lib.w4a16_moe_run_stage_ex(stage, *args(i), tptr))
             torch.cuda.current_stream().wait_stream(s)
+            # `replays` cycles over the sets in one graph: the replay overhead
+            # is spread over all of its launches
             with torch.cuda.graph(g):
-                for i in range(len(self.sets)):
-                    L.check(lib.w4a16_moe_run_stage_ex(stage, *args(i), tptr))
+                for _ in range(replays):
+                    for i in range(len(self.sets)):
+                        L.check(lib.w4a16_moe_run_stage_ex(stage, *args(i), tptr))
             g.replay()
             torch.cuda.synchronize()
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             start.record()
-            for _ in range(replays):
-                g.replay()
+            g.replay()
             end.record()
             torch.cuda.synchronize()
             result[name] = start.elapsed_time(end) / (replays * len(self.sets))
+            del g
         del wss, outs
         return result
 
@@ -220,16 +226,16 @@ def time_router(wl, replays):
         wl.pkg.router_topk_softmax(x, shape.topk, out=o)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for x, o in zip(sets, outs):
-            wl.pkg.router_topk_softmax(x, shape.topk, out=o)
+    with torch.cuda.graph(g):  # `replays` cycles in one graph
+        for _ in range(replays):
+            for x, o in zip(sets, outs):
+                wl.pkg.router_topk_softmax(x, shape.topk, out=o)
     g.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(replays):
-        g.replay()
+    g.replay()
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / (replays * len(sets))
