@@ -193,16 +193,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //      step, lane l's 16 bytes at l * 16.
 //   S  2 slots x 8 waves x 1 KB: a wave's scales of one loop iteration (8
 //      groups of 32 elements), lane l's bytes at l times the DMA size.
-//   D  1 KB that the surplus activation DMAs of odd token-block counts write
-//      (never read), so that every wave issues the same DMAs per step.
 constexpr int kWaves = 8;
 constexpr int kWslots = 4;
 constexpr int kWslot = kWaves * 1024;
 constexpr int kSslot = kWaves * 1024;
 constexpr int kOffW = kAbufs * kAbuf;
 constexpr int kOffS = kOffW + kWslots * kWslot;
-constexpr int kOffD = kOffS + 2 * kSslot;
-constexpr int kLdsTotal = kOffD + 1024;
+constexpr int kLdsTotal = kOffS + 2 * kSslot;
 static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
 
 // One tile of MC token blocks (32 slots each).  GSHIFT = log2(group / 32).
@@ -222,7 +219,7 @@ static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
 // t - 2, after that step's activation DMAs) has landed -- the vector-memory
 // count of the instructions behind it is exact below -- and the workgroup
 // barrier then makes every wave's activation rows visible.
-template <int MODE, int GSHIFT, int MC>
+template <int MODE, int GSHIFT, int MC, int NA>
 __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, int nrt,
                                          const int* s_f, unsigned char* lds) {
   const int tid = threadIdx.x;
@@ -245,22 +242,19 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   };
 
   // ---- activation DMA: the tile's 4 MC DMAs of 1 KB (8 rows each) are dealt
-  // round robin over the 8 waves, NA per wave; DMA k fills rows 8 k .. 8 k + 7
-  // of the buffer: lane l writes row r = 8 k + l / 8 at chunk position l % 8,
-  // so it fetches chunk (l % 8) ^ g(r) of that row.  A wave's surplus DMA
-  // (odd MC) repeats its first one into the dummy region.  Rows of padding
-  // slots read row 0.
-  constexpr int NA = (4 * MC + kWaves - 1) / kWaves;
-  uint32_t a_off[NA];  // byte offset of this lane's source row + chunk
-  int a_dst[NA];       // LDS byte offset within a buffer, or -1: dummy
+  // round robin over the 8 waves, so wave w issues NA = ceil((4 MC - w) / 8)
+  // of them (the caller instantiates both counts of an odd MC); DMA k fills
+  // rows 8 k .. 8 k + 7 of the buffer: lane l writes row r = 8 k + l / 8 at
+  // chunk position l % 8, so it fetches chunk (l % 8) ^ g(r) of that row.
+  // Rows of padding slots read row 0.
+  static_assert(NA >= 0 && NA <= (4 * MC + kWaves - 1) / kWaves, "activation DMAs per wave");
+  constexpr int kNA1 = NA > 0 ? NA : 1;
+  uint32_t a_off[kNA1];  // byte offset of this lane's source row + chunk
+  int a_dst[kNA1];       // LDS byte offset within a buffer
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    int k = kWaves * i + wid;
+    const int k = kWaves * i + wid;  // < 4 MC for this wave's NA
     a_dst[i] = k * 1024;
-    if (k >= 4 * MC) {
-      k = wid;
-      a_dst[i] = -1;
-    }
     const int r = 8 * k + (lane >> 3);
     const int f = s_f[r];
     uint32_t row = 0;
@@ -272,8 +266,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // The item's row tiles share the activation rows: local step k of any.
   auto dma_a1 = [&](int k, int buf, int i) {
     const uint32_t koff = (uint32_t)k * (kStepK * 2);
-    lds_dma16(act, a_off[i] + koff,
-              lds_addr(lds + (a_dst[i] < 0 ? kOffD : buf * kAbuf + a_dst[i])));
+    lds_dma16(act, a_off[i] + koff, lds_addr(lds + buf * kAbuf + a_dst[i]));
   };
   auto dma_a = [&](int k, int buf) {
 #pragma unroll
@@ -575,15 +568,26 @@ void mfma_kernel(const MfmaLaunch a) {
     s_f[i] = i < count ? a.sorted[start + i] : a.n_tok;
   __syncthreads();
 
+  // Wave w issues ceil((4 MC - w) / 8) activation DMAs per step: for odd MC
+  // the first (4 MC) % 8 waves one more than the others.
+  const int wid = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+#define W4A16_MFMA_TILE(MC_)                                                            \
+  case MC_:                                                                             \
+    if (wid < (4 * MC_) % kWaves)                                                       \
+      run_tile<MODE, GSHIFT, MC_, (4 * MC_ + kWaves - 1) / kWaves>(a, e, nt0, nrt, s_f, lds); \
+    else                                                                                \
+      run_tile<MODE, GSHIFT, MC_, (4 * MC_) / kWaves>(a, e, nt0, nrt, s_f, lds);        \
+    break;
   switch ((count + 31) >> 5) {
-    case 1: run_tile<MODE, GSHIFT, 1>(a, e, nt0, nrt, s_f, lds); break;
-    case 2: run_tile<MODE, GSHIFT, 2>(a, e, nt0, nrt, s_f, lds); break;
-    case 3: run_tile<MODE, GSHIFT, 3>(a, e, nt0, nrt, s_f, lds); break;
-    case 4: run_tile<MODE, GSHIFT, 4>(a, e, nt0, nrt, s_f, lds); break;
-    case 5: run_tile<MODE, GSHIFT, 5>(a, e, nt0, nrt, s_f, lds); break;
-    case 6: run_tile<MODE, GSHIFT, 6>(a, e, nt0, nrt, s_f, lds); break;
+    W4A16_MFMA_TILE(1)
+    W4A16_MFMA_TILE(2)
+    W4A16_MFMA_TILE(3)
+    W4A16_MFMA_TILE(4)
+    W4A16_MFMA_TILE(5)
+    W4A16_MFMA_TILE(6)
     default: break;
   }
+#undef W4A16_MFMA_TILE
 }
 
 template <int MODE>
