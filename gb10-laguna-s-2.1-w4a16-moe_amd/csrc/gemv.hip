@@ -400,6 +400,12 @@ void gemv_kernel(const GemvLaunch a) {
 
     for (int t0 = 0; t0 < T; t0 += NTOK) {
       const int tc = min(NTOK, T - t0);  // tokens past tc compute unused values
+      // w2: the pair this lane stores and its routing weight, loaded here so
+      // that the load overlaps the weight stream instead of ending it.  (w13
+      // finds its pair only at the end: one more live register there would
+      // cost its 4-token variant a wave per SIMD.)
+      const int f_pre = MODE == 1 ? slot_of(min(t0 + sl, T - 1)) : 0;
+      const float wt_mine = MODE == 1 ? a.topk_w[f_pre] : 0.0f;
       // Opaque row offsets per pass: otherwise every load address of the pass
       // is loop-invariant, gets hoisted out of the pass loop and stays live
       // in registers for the whole kernel.
@@ -439,7 +445,7 @@ void gemv_kernel(const GemvLaunch a) {
         bool valid;
         const int cu = unit_chunk(u, valid);
         const int nb = cu * rows_per_wave + r;
-        const int f_mine = slot_of(min(t0 + sl, T - 1));
+        const int f_mine = MODE == 1 ? f_pre : slot_of(min(t0 + sl, T - 1));
         if (valid && sl < tc) {
           float v[NR];
 #pragma unroll
@@ -455,7 +461,7 @@ void gemv_kernel(const GemvLaunch a) {
             for (int q = 0; q < RPL; ++q)
               out[nb + RG * q] = (uint16_t)f32_to_bf16(silu(v[q]) * v[RPL + q]);
           } else {
-            const float wt = a.topk_w[f_mine];
+            const float wt = wt_mine;
             if (a.partial_bf16) {
               uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f_mine * a.n_out;
 #pragma unroll
@@ -543,6 +549,7 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
 
   const int E = a.num_experts;
   const int e_raw = a.ids[f];
+  const float wt = a.topk_w[f];  // loaded with the id, used at the end
   const bool valid = e_raw >= 0 && e_raw < E;  // wave-uniform
   const int e = valid ? e_raw : 0;
   stage_row<64>(a.act + (int64_t)f * a.ld_act, kdim, xp, xc, lane);
@@ -602,14 +609,15 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
     }
   }
   acc = oct_sum(acc);
-  if (sl == 0) red[t * 8 + r] = acc * a.topk_w[f];
+  // A slot routed outside [0, E) parks +0.0: the sum starts at +0.0 and so
+  // is never -0.0, and adding +0.0 to any other value leaves it unchanged,
+  // so summing every slot equals skipping those -- without reading the ids
+  // again here.
+  if (sl == 0) red[t * 8 + r] = valid ? acc * wt : 0.0f;
   __syncthreads();
   if (threadIdx.x < 8) {
     float sum = 0.0f;
-    for (int s = 0; s < topk; ++s) {
-      const int es = a.ids[m * topk + s];
-      if (es >= 0 && es < E) sum += red[s * 8 + threadIdx.x];
-    }
+    for (int s = 0; s < topk; ++s) sum += red[s * 8 + threadIdx.x];
     out[(int64_t)m * ld_out + blockIdx.x * 8 + threadIdx.x] = (uint16_t)f32_to_bf16(sum);
   }
 }
