@@ -142,6 +142,9 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
 // gets in fl[j] the flat index of the expert's pair of rank l + 64 j (n_tok
 // past the last).  e_out = -1 when the item has no work; dropped = pairs with
 // ids outside [0, E).  Requires 1 <= n_tok <= kRouteMaxTok.
+// NQ: ids per lane actually read (1 when n_tok <= 64, else 4); the lanes'
+// further ids count as absent.
+template <int NQ>
 __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e_out,
                                            int& t_out, int (&fl)[4], int& dropped) {
   const int lane = __lane_id();
@@ -151,7 +154,8 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
 #pragma unroll
   for (int q = 0; q < 4; ++q) {  // clamped loads, all in flight together
     const int f = lane + 64 * q;
-    const int v = a.ids[min(f, n_tok - 1)];
+    int v = kNone;
+    if (q < NQ) v = a.ids[min(f, n_tok - 1)];
     id[q] = f < n_tok ? v : kNone;
   }
   int drop = 0;
@@ -249,7 +253,10 @@ void gemv_kernel(const GemvLaunch a) {
   int fl[4];
   if constexpr (ROUTE) {
     int dropped;
-    route_wave(a, item, e, T, fl, dropped);
+    if (a.n_tok <= 64)
+      route_wave<1>(a, item, e, T, fl, dropped);
+    else
+      route_wave<4>(a, item, e, T, fl, dropped);
     if (MODE == 0 && blockIdx.x == 0 && tid == 0) a.dropped_out[0] = dropped;
     if (e < 0) return;  // workgroup-uniform: every wave routes the same item
   } else {
