@@ -12,13 +12,15 @@ headline value is BASELINE.json's configs[1]: E=256, top-10, K=3072, N=1024,
 group 32, M=16 tokens, uniform routing.  The other configurations are reported
 in "configs".
 
-Timing: the K timed calls are captured as one HIP graph (chunks of at most
-2048 calls) that cycles through several routing/hidden sets, so the touched
-weights exceed the 256 MB Infinity Cache several times over and the graph's
-per-replay overhead is spread over all K calls, as in a serving loop that
-captures a whole forward pass; W warmup calls and one untimed replay, then
-exactly K timed calls bracketed by device synchronisation and events on the
-capturing stream.
+Timing (the reference's protocol, bench/bench_moe.py:475-512, on a graph of
+K calls): W eager warm-up calls; the K calls captured as one HIP graph (chunks
+of at most 2048 calls) that cycles through several routing/hidden sets, so
+the touched weights exceed the 256 MB Infinity Cache several times over;
+warm-up replays of that graph until at least 200 ms of device time has run
+(a GPU that was idle runs its first ~15 ms of work up to 15 % slower while its
+clocks ramp up); then R timed replays back to back, each bracketed by events
+on the launch stream, the whole timed region bracketed by device
+synchronisation.  The reported time per call is the p50 replay / K.
 
 Per-kernel durations come from graphs of one stage at a time
 (w4a16_moe_run_stage_ex, with the dispatch tuning the call itself uses) that
@@ -65,6 +67,9 @@ MALL_BYTES = 256 * 2**20       # Infinity Cache
 # 226.3 GB/s on NVIDIA GB10 (results/showdown2.json:1104; README.md:62-70).
 REFERENCE_GBS_M16 = 226.3
 STAGES = ("align", "w13", "w2", "combine")
+WARM_MS = 200.0                # device time of warm-up replays before the timed ones
+TIMED_MS = 250.0               # device time the timed replays aim for ...
+MIN_REPLAYS, MAX_REPLAYS = 9, 50   # ... within these replay counts
 CALIB_BYTES = 2**30            # plain device copy: PMC byte-counter scale and measured copy BW
 # Kernel-name fragments of the dominant kernels in rocprofv3 counter files,
 # per stage and path (dequant-GEMV for few pairs per expert, MFMA tiles else).
@@ -109,7 +114,8 @@ class Workload:
                                             self.shape.group)
 
     # ---- whole-call timing (the headline) ----------------------------------
-    def time_calls(self, steps, warmup):
+    def time_calls(self, steps, warmup, replays=None, warm_ms=WARM_MS):
+        """p50 over `replays` timed replays of one graph of `steps` calls."""
         import torch
 
         n = len(self.sets)
@@ -118,8 +124,7 @@ class Workload:
         torch.cuda.synchronize()
         # The timed calls are captured as one graph of exactly `steps` calls
         # cycling through the sets (chunks of at most kMaxGraph calls), as a
-        # serving loop captures a whole forward pass: the per-replay launch
-        # overhead is then spread over every call, not over one set cycle.
+        # serving loop captures a whole forward pass.
         kMaxGraph = 2048
         chunks = [min(kMaxGraph, steps - s0) for s0 in range(0, steps, kMaxGraph)]
         stream = torch.cuda.Stream()
@@ -136,28 +141,53 @@ class Workload:
                 for i in range(c):
                     self.call(i % n)
             graphs[c] = g
-        # one untimed pass so first-replay costs stay out of the timed region
-        for c in chunks:
-            graphs[c].replay()
+
+        def replay():
+            for c in chunks:
+                graphs[c].replay()
+
+        ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+        # Warm-up replays until warm_ms of device time has run.
+        a, b = ev(), ev()
+        a.record()
+        replay()
+        b.record()
         torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        one_ms = a.elapsed_time(b)
+        n_warm = max(2, math.ceil(warm_ms / max(one_ms, 1e-3)))
+        for _ in range(n_warm - 1):
+            replay()
+        if replays is None:
+            replays = min(MAX_REPLAYS, max(MIN_REPLAYS, math.ceil(TIMED_MS / max(one_ms, 1e-3))))
+        evs = [ev() for _ in range(replays + 1)]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        start.record()
-        for c in chunks:
-            graphs[c].replay()
-        end.record()
+        evs[0].record()
+        for i in range(replays):
+            replay()
+            evs[i + 1].record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        ms = start.elapsed_time(end)
+        per = [evs[i].elapsed_time(evs[i + 1]) for i in range(replays)]
+        p50 = sorted(per)[len(per) // 2]
         nbytes = sum(self.bytes[i % n] for c in chunks for i in range(c))
         del graphs
-        return {"elapsed_ms": ms, "wall_s": wall, "steps": steps, "bytes": nbytes}
+        return {"elapsed_ms": p50, "wall_s": wall, "steps": steps, "bytes": nbytes,
+                "replays": replays, "warmup_replays": n_warm,
+                "replay_ms": {"p50": round(p50, 4), "min": round(min(per), 4),
+                              "max": round(max(per), 4), "mean": round(sum(per) / len(per), 4)}}
 
     # ---- per-stage timing ---------------------------------------------------
-    def time_stages(self, replays):
-        """Average device time per launch of each stage, over all sets."""
+    def stage_launches(self):
+        """Kernel launches of each stage (sort, w13, w2, combine) of this M."""
+        shape = self.shape
+        ts = None if self.tuning is None else self.tuning.to_struct()
+        return self.pkg._lib.stage_launches(self.cfg.M, shape.topk, shape.E, shape.N, shape.K,
+                                            shape.group, ts)
+
+    def time_stages(self, replays, timed=5):
+        """Average device time per launch of each stage, over all sets (None
+        for a stage that launches no kernel at this M)."""
         import torch
 
         lib = self.pkg._lib.lib()
@@ -181,8 +211,12 @@ class Workload:
         for i in range(len(self.sets)):
             L.check(lib.w4a16_moe_fused_experts_ex(*args(i), tptr))
         torch.cuda.synchronize()
+        launches = self.stage_launches()
         result = {}
         for stage, name in enumerate(STAGES):
+            if launches[stage] == 0:
+                result[name] = None
+                continue
             g = torch.cuda.CUDAGraph()
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
@@ -197,14 +231,15 @@ class Workload:
                     for i in range(len(self.sets)):
                         L.check(lib.w4a16_moe_run_stage_ex(stage, *args(i), tptr))
             g.replay()
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(timed + 1)]
             torch.cuda.synchronize()
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record()
-            g.replay()
-            end.record()
+            evs[0].record()
+            for k in range(timed):
+                g.replay()
+                evs[k + 1].record()
             torch.cuda.synchronize()
-            result[name] = start.elapsed_time(end) / (replays * len(self.sets))
+            per = sorted(evs[k].elapsed_time(evs[k + 1]) for k in range(timed))
+            result[name] = per[timed // 2] / (replays * len(self.sets))
             del g
         del wss, outs
         return result
@@ -261,14 +296,68 @@ def summarize(wl, t, stages):
         "TFLOP_s": round(tflops, 3),
         "pct_bf16_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 3),
         "tuning": "built-in" if wl.tuning is None else wl.tuning.to_dict(),
+        "timing": {"calls_per_replay": t["steps"], "timed_replays": t["replays"],
+                   "warmup_replays": t["warmup_replays"], "replay_ms": t["replay_ms"]},
     }
     if stages is not None:
-        row["stage_us"] = {k: round(v * 1e3, 3) for k, v in stages.items()}
+        row["stage_us"] = {k: (None if v is None else round(v * 1e3, 3))
+                           for k, v in stages.items()}
         w13 = sum(wl.w13_bytes) / len(wl.w13_bytes)
         w2 = sum(wl.w2_bytes) / len(wl.w2_bytes)
         row["stage_GB_s"] = {"w13": round(w13 / (stages["w13"] * 1e-3) / 1e9, 2),
                              "w2": round(w2 / (stages["w2"] * 1e-3) / 1e9, 2)}
     return row
+
+
+def parity_row(wl, cpu_budget_s, max_calls=9):
+    """Set 0 of a workload against the oracle: the GPU output against the
+    PyTorch CPU dequant reference (bench/bench_moe.py:271-303, errors as
+    bench/bench_moe.py:520-527 computes them, plus max-abs over max|ref|),
+    that reference's CPU time (p50 of as many calls as fit cpu_budget_s, at
+    least one), and the expert sort against the oracle's
+    moe_align_block_size (kernels/w4a16_moe.py:187-290), bit for bit."""
+    import numpy as np
+    import torch
+
+    from oracle import moe_oracle as orc
+
+    shape = wl.shape
+    x, tw, ti = wl.sets[0]
+    out = wl.call(0)
+    torch.cuda.synchronize()
+    out32 = out.float().cpu()
+    xc, twc, tic = x.cpu(), tw.cpu(), ti.cpu()
+    times, ref = [], None
+    while not times or (sum(times) < cpu_budget_s and len(times) < max_calls):
+        t0 = time.perf_counter()
+        ref = orc.moe_reference(xc, *wl.wcpu, twc, tic, shape.group, out_dtype=None)
+        times.append(time.perf_counter() - t0)
+    cpu_s = sorted(times)[len(times) // 2]
+    max_ref = float(ref.abs().max())
+    mab = orc.max_abs(out32, ref)
+    # The sort the fused call runs (block 16), standalone, and the one inside
+    # the call's workspace when the call runs it (M above the GEMV-only bound).
+    want = orc.moe_align_block_size(tic.numpy(), wl.pkg._lib.FUSED_BLOCK_M, shape.E)
+    got = wl.pkg.moe_align_block_size_full(ti, wl.pkg._lib.FUSED_BLOCK_M, shape.E)
+    torch.cuda.synchronize()
+    routing_exact = all(np.array_equal(g.cpu().numpy(), w) for g, w in zip(got[:4], want[:4]))
+    internal = None
+    if wl.stage_launches()[0] > 0:
+        ws, off = wl.pkg.workspace_tensor(x, ti, wl.w13, wl.w2, shape.group, tuning=wl.tuning)
+        em, nb = want[0].size, want[1].size
+        fields = (ws[off[0]: off[0] + 4 * em], ws[off[1]: off[1] + 4 * nb],
+                  ws[off[2]: off[2] + 4], ws[off[3]: off[3] + 4 * (shape.E + 1)])
+        internal = all(np.array_equal(f.view(torch.int32).cpu().numpy(), w)
+                       for f, w in zip(fields, want[:4]))
+    return {
+        "parity": {"rel_l2": orc.rel_l2(out32, ref), "max_abs": mab, "max_ref": max_ref,
+                   "max_abs_over_max_ref": mab / max_ref if max_ref else None,
+                   "routing_bit_exact": routing_exact, "internal_sort_bit_exact": internal,
+                   "oracle": "oracle.moe_reference (fp32, bf16-rounded dequantized weights), "
+                             "routing set 0"},
+        "cpu": {"us_per_call": round(cpu_s * 1e6, 1), "cores": torch.get_num_threads(),
+                "calls": len(times), "kind": "port"},
+    }
 
 
 def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
@@ -279,7 +368,7 @@ def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
 
     threads = torch.get_num_threads()
     x, tw, ti = (t.cpu() for t in wl.sets[0])
-    w = tuple(t.cpu() for t in (wl.w13, wl.w2, wl.s13, wl.s2))
+    w = wl.wcpu
     gpu_out = wl.call(0).float().cpu()
     t0 = time.perf_counter()
     ref = orc.moe_reference(x, *w, tw, ti, wl.shape.group)  # warmup
@@ -299,7 +388,9 @@ def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
         "kind": "port",
         "sample": (f"oracle.moe_reference (PyTorch CPU dequant reference) on routing set 0 of "
                    f"config {wl.cfg.index} (M={wl.cfg.M}, {wl.touched[0]} touched experts), "
-                   f"1 warmup + {len(timed)} timed calls, p50 {p50 * 1e3:.1f} ms"),
+                   f"1 warmup + {len(timed)} timed calls, p50 {p50 * 1e3:.1f} ms; each "
+                   f"config row's \"cpu\" field times the same reference on that config "
+                   f"(config 0, M=1, is the one BASELINE.md names)"),
         "cpu": platform.processor() or platform.machine(),
         "gpu_vs_cpu_rel_l2": orc.rel_l2(gpu_out, ref32),
         "gpu_vs_cpu_max_abs": orc.max_abs(gpu_out, ref32),
@@ -445,6 +536,11 @@ def main(argv=None) -> int:
     p.add_argument("--sets", type=int, default=None, help="routing sets to cycle through")
     p.add_argument("--no-sweep", action="store_true", help="skip the other configs")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--replays", type=int, default=None,
+                   help=f"timed replays of the K-call graph (default: enough for "
+                        f"{TIMED_MS:.0f} ms, {MIN_REPLAYS}..{MAX_REPLAYS})")
+    p.add_argument("--no-parity", action="store_true",
+                   help="skip the per-config oracle comparison and CPU timing")
     p.add_argument("--stage-replays", type=int, default=8)
     p.add_argument("--calibrate-copy", action="store_true",
                    help=f"run one {CALIB_BYTES >> 20} MiB device copy first (PMC calibration)")
@@ -477,15 +573,25 @@ def main(argv=None) -> int:
     weights = synth.make_weights(shape, dev, seed=0)
     torch.cuda.synchronize()
 
+    wcpu = None if args.no_parity and args.no_cpu_baseline else tuple(t.cpu() for t in weights)
+
+    def parity(w, budget):
+        if args.no_parity:
+            return {}
+        return parity_row(w, budget)
+
     head_cfg = synth.CONFIGS[args.config]
     wl = Workload(pkg, synth, shape, weights, head_cfg, dev, n_sets=args.sets)
+    wl.wcpu = wcpu
     log(f"config {head_cfg.index} ({head_cfg.description}): {len(wl.sets)} sets, "
         f"avg touched experts {sum(wl.touched) / len(wl.touched):.1f}")
-    t = wl.time_calls(args.steps, args.warmup)
-    log(f"timed {t['steps']} steps in {t['elapsed_ms']:.3f} ms (wall {t['wall_s']:.3f} s)")
+    t = wl.time_calls(args.steps, args.warmup, args.replays)
+    log(f"timed {t['replays']} replays of {t['steps']} calls after {t['warmup_replays']} "
+        f"warm-up replays: {json.dumps(t['replay_ms'])} ms per replay (wall {t['wall_s']:.3f} s)")
     stages = wl.time_stages(args.stage_replays)
     head = summarize(wl, t, stages)
     head["router"] = time_router(wl, 20)
+    head.update(parity(wl, 5.0))
     log(f"headline: {json.dumps(head)}")
 
     dominant = "w13" if stages["w13"] >= stages["w2"] else "w2"
@@ -507,15 +613,21 @@ def main(argv=None) -> int:
                 sweep.append(head)
                 continue
             w = Workload(pkg, synth, shape, weights, cfg, dev)
+            w.wcpu = wcpu
             steps = len(w.sets) * (4 if cfg.M <= 64 else 2)
             tt = w.time_calls(steps, min(8, len(w.sets)))
             st = w.time_stages(2)
             row = summarize(w, tt, st)
             row["router"] = time_router(w, 20)
+            row.update(parity(w, 5.0 if cfg.M <= 64 else 0.0))
             log(f"config {cfg.index}: {json.dumps(row)}")
             sweep.append(row)
             del w
             torch.cuda.empty_cache()
+    for row in sweep:
+        if "cpu" in row:
+            row["cpu"]["speedup_gpu_vs_cpu"] = round(row["cpu"]["us_per_call"] /
+                                                     row["us_per_call"], 1)
 
     copy_bw = measured_copy_bw(dev)
     log(f"measured device copy: {copy_bw['GB_s']} GB/s")
@@ -535,6 +647,13 @@ def main(argv=None) -> int:
         "steps": t["steps"],
         "warmup": args.warmup,
         "ms_per_step": round(t["elapsed_ms"] / t["steps"], 6),
+        "timing": {"protocol": ("p50 over timed replays of one HIP graph of `steps` calls, "
+                                "after `warmup` eager calls and warm-up replays of that graph "
+                                f"(>= {WARM_MS:.0f} ms of device time); replays back to back, "
+                                "events on the launch stream, device synchronisation around "
+                                "the timed region"),
+                   "timed_replays": t["replays"], "warmup_replays": t["warmup_replays"],
+                   "replay_ms": t["replay_ms"]},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(value / REFERENCE_GBS_M16, 3) if head_cfg.index == 1 else None,

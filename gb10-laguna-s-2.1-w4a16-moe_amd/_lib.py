@@ -59,6 +59,8 @@ EXPORTED_SYMBOLS = (
     "w4a16_moe_workspace_size_ex",
     "w4a16_moe_fused_experts_ex",
     "w4a16_moe_run_stage_ex",
+    "w4a16_moe_workspace_layout_ex",
+    "w4a16_moe_stage_launches",
     "w4a16_moe_strerror",
     "w4a16_moe_abi_version",
 )
@@ -118,6 +120,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.w4a16_moe_fused_experts_ex.argtypes = fused + [tp]
     lib.w4a16_moe_run_stage_ex.restype = ctypes.c_int
     lib.w4a16_moe_run_stage_ex.argtypes = [ctypes.c_int] + fused + [tp]
+    lib.w4a16_moe_workspace_layout_ex.restype = ctypes.c_int
+    lib.w4a16_moe_workspace_layout_ex.argtypes = [_i64] * 6 + [tp, ctypes.POINTER(ctypes.c_size_t)]
+    lib.w4a16_moe_stage_launches.restype = ctypes.c_int
+    lib.w4a16_moe_stage_launches.argtypes = [_i64] * 6 + [tp, ctypes.POINTER(ctypes.c_int32)]
     lib.w4a16_moe_router_topk_softmax.restype = ctypes.c_int
     lib.w4a16_moe_router_topk_softmax.argtypes = [
         _vp, ctypes.c_int, _i64, _i64, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]
@@ -178,6 +184,23 @@ def default_tuning(M: int, topk: int, E: int, N: int, K: int, group: int) -> Tun
 def workspace_layout(M: int, topk: int, E: int, N: int, K: int, group: int) -> list[int]:
     arr = (ctypes.c_size_t * WS_NFIELDS)()
     check(lib().w4a16_moe_workspace_layout(M, topk, E, N, K, group, arr))
+    return list(arr)
+
+
+def workspace_layout_ex(M: int, topk: int, E: int, N: int, K: int, group: int,
+                        tuning: "TuningStruct | None") -> list[int]:
+    arr = (ctypes.c_size_t * WS_NFIELDS)()
+    ptr = ctypes.byref(tuning) if tuning is not None else None
+    check(lib().w4a16_moe_workspace_layout_ex(M, topk, E, N, K, group, ptr, arr))
+    return list(arr)
+
+
+def stage_launches(M: int, topk: int, E: int, N: int, K: int, group: int,
+                   tuning: "TuningStruct | None") -> list[int]:
+    """Kernel launches of each stage (sort, w13, w2, combine) of such a call."""
+    arr = (ctypes.c_int32 * 4)()
+    ptr = ctypes.byref(tuning) if tuning is not None else None
+    check(lib().w4a16_moe_stage_launches(M, topk, E, N, K, group, ptr, arr))
     return list(arr)
 
 

@@ -12,6 +12,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -25,7 +26,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-mcode-object-version=5",
     # Packed fp32 VALU forms stay off: hand-written and compiler-made
     # v_pk_{add,mul,fma}_f32 are excluded from every kernel here.
@@ -46,26 +46,36 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    if verbose and proc.stderr.strip():
+        noise = "is not a recognized feature for this target"
+        lines = [ln for ln in proc.stderr.splitlines() if noise not in ln]
+        if lines:
+            print("\n".join(lines), file=sys.stderr, flush=True)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile all HIP sources into LIB_PATH (atomic replace)."""
+    """Compile every HIP source to an object (in parallel), link them into
+    LIB_PATH (atomic replace)."""
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    cc = hipcc()
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with tempfile.TemporaryDirectory(dir=PKG_DIR) as tmp:
+        objs = [Path(tmp) / (src.stem + ".o") for src in srcs]
+        with ThreadPoolExecutor(max_workers=jobs) as ex:
+            for f in [ex.submit(_run, [cc, *HIPCC_FLAGS, "-c", "-o", str(o), str(src)], verbose)
+                      for src, o in zip(srcs, objs)]:
+                f.result()
         tmp_lib = Path(tmp) / LIB_NAME
-        cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp_lib), *map(str, srcs)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise RuntimeError(
-                f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}"
-            )
-        if verbose and proc.stderr.strip():
-            noise = "is not a recognized feature for this target"
-            lines = [ln for ln in proc.stderr.splitlines() if noise not in ln]
-            if lines:
-                print("\n".join(lines), file=sys.stderr, flush=True)
+        _run([cc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib),
+              *map(str, objs)], verbose)
         os.replace(tmp_lib, LIB_PATH)
     return LIB_PATH
 

@@ -251,6 +251,15 @@ struct FusedArgs {
   const w4a16_moe_tuning* tuning;  // null: built-in choices
 };
 
+// The MFMA kernels address activation rows with 32-bit byte offsets from the
+// row base: the last hidden row (w13) and the last intermediate row (w2) must
+// start below this.
+constexpr int64_t kMfmaActBytesMax = (int64_t)UINT32_MAX - 4096;
+
+bool mfma_act_fits(int64_t M, int64_t topk, int64_t N, int64_t ld_hidden) {
+  return M * ld_hidden * 2 <= kMfmaActBytesMax && M * topk * N * 2 <= kMfmaActBytesMax;
+}
+
 int validate(const FusedArgs& a, Layout* L) {
   Tuning T;
   int st = resolve_tuning(a.tuning, &T);
@@ -263,6 +272,7 @@ int validate(const FusedArgs& a, Layout* L) {
       !a.out || !a.ws)
     return W4A16_ERR_NULL_POINTER;
   if (a.ld_hidden < a.K || a.ld_out < a.K) return W4A16_ERR_INVALID_SHAPE;
+  if (L->mfma && !mfma_act_fits(a.M, a.topk, a.N, a.ld_hidden)) return W4A16_ERR_INVALID_SHAPE;
   if (a.ws_bytes < L->total) return W4A16_ERR_WORKSPACE_TOO_SMALL;
   if (!aligned(a.hidden, 16) || a.ld_hidden % 8 != 0) return W4A16_ERR_MISALIGNED;
   if (!aligned(a.w13, 16) || !aligned(a.w2, 16)) return W4A16_ERR_MISALIGNED;
@@ -514,14 +524,46 @@ int w4a16_moe_workspace_size(int64_t M, int64_t topk, int64_t num_experts, int64
                                      bytes);
 }
 
+int w4a16_moe_workspace_layout_ex(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                                  int64_t K, int64_t group_size,
+                                  const w4a16_moe_tuning* tuning,
+                                  size_t offsets[W4A16_WS_NFIELDS]) {
+  if (!offsets) return W4A16_ERR_NULL_POINTER;
+  Tuning T;
+  int st = resolve_tuning(tuning, &T);
+  if (st) return st;
+  Layout L;
+  st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L);
+  if (st) return st;
+  for (int i = 0; i < W4A16_WS_NFIELDS; ++i) offsets[i] = L.off[i];
+  return W4A16_OK;
+}
+
 int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
                                int64_t K, int64_t group_size,
                                size_t offsets[W4A16_WS_NFIELDS]) {
-  if (!offsets) return W4A16_ERR_NULL_POINTER;
-  Layout L;
-  const int st = compute_layout(M, topk, num_experts, N, K, group_size, default_tuning(), &L);
+  return w4a16_moe_workspace_layout_ex(M, topk, num_experts, N, K, group_size, nullptr,
+                                       offsets);
+}
+
+int w4a16_moe_stage_launches(int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                             int64_t K, int64_t group_size, const w4a16_moe_tuning* tuning,
+                             int32_t launches[4]) {
+  if (!launches) return W4A16_ERR_NULL_POINTER;
+  Tuning T;
+  int st = resolve_tuning(tuning, &T);
   if (st) return st;
-  for (int i = 0; i < W4A16_WS_NFIELDS; ++i) offsets[i] = L.off[i];
+  Layout L;
+  st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L);
+  if (st) return st;
+  for (int i = 0; i < 4; ++i) launches[i] = 0;
+  if (M == 0) return W4A16_OK;
+  // The same decisions as run_fused (scales assumed 16-byte aligned, as
+  // torch allocations are).
+  launches[0] = L.route ? 0 : (L.chunked ? 2 : 1);
+  launches[1] = (L.gemv ? 1 : 0) + (L.mfma ? 1 : 0);
+  launches[2] = L.token ? 1 : (L.gemv ? 1 : 0) + (L.mfma ? 1 : 0);
+  launches[3] = L.token ? 0 : 1;
   return W4A16_OK;
 }
 

@@ -534,8 +534,10 @@ void gemv_kernel(const GemvLaunch a) {
 // fma per group, the same 8-lane sum), multiplies by the routing weight and
 // parks the value in LDS.  The workgroup then adds the slots in order from
 // 0.0, skipping ids outside [0, E), as combine_kernel does.  The result is
-// therefore bit-identical to gemv_kernel + combine_kernel, with one launch,
-// no partial rows in memory, and every wave's weight loads in flight at once.
+// therefore bit-identical to gemv_kernel + combine_kernel (with the same
+// bf16 rounding of each weighted slot value when the call keeps bf16 partial
+// rows), with one launch, no partial rows in memory, and every wave's weight
+// loads in flight at once.
 template <int NIT>
 __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint16_t* out,
                                                        int64_t ld_out) {
@@ -616,11 +618,15 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
     }
   }
   acc = oct_sum(acc);
+  // The weighted slot value is rounded to bf16 when the call keeps bf16
+  // partial rows (M > 4), as gemv_kernel<1> stores it for combine_kernel.
+  float v = acc * wt;
+  if (a.partial_bf16) v = bf16_to_f32(f32_to_bf16(v));
   // A slot routed outside [0, E) parks +0.0: the sum starts at +0.0 and so
   // is never -0.0, and adding +0.0 to any other value leaves it unchanged,
   // so summing every slot equals skipping those -- without reading the ids
   // again here.
-  if (sl == 0) red[t * 8 + r] = valid ? acc * wt : 0.0f;
+  if (sl == 0) red[t * 8 + r] = valid ? v : 0.0f;
   __syncthreads();
   if (threadIdx.x < 8) {
     float sum = 0.0f;

@@ -230,7 +230,7 @@ def tune(ms, E, N, K, group, topk, seed=0, check_tol=5e-3):
             f"(built-in {base_us['uniform']:.1f}), skewed {best[2]['skewed']:.1f} us "
             f"(built-in {base_us['skewed']:.1f})")
         del benches, refs
-        pkg.w4a16_moe._WS_CACHE.clear()  # one workspace per candidate was cached
+        pkg.w4a16_moe._WS_POOL.clear()  # the candidates' graphs are gone
         torch.cuda.empty_cache()
     return table, report
 

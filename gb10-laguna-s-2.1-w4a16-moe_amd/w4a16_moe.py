@@ -34,8 +34,60 @@ BLOCK_M = 16
 BLOCK_N = 64
 BLOCK_K = 64
 
-_WS_CACHE: dict[tuple, torch.Tensor] = {}
-_WS_LOCK = threading.Lock()
+
+
+class WorkspacePool:
+    """Workspaces of the fused call: one buffer per (device, stream), grown to
+    the largest size a call has needed and reused by every smaller call.
+
+    The reference pools its scratch per (device, M, ...) shape
+    (kernels/w4a16_moe.py:293-316), which keeps one buffer per distinct M for
+    the life of the process.  Calls on one stream run in order, so they can
+    share one buffer; calls on different streams get different buffers (the
+    C ABI's rule: calls sharing a workspace must not overlap).  A buffer that
+    a HIP graph captured stays alive when the pool grows past it, since the
+    graph's kernels keep its address.
+    """
+
+    def __init__(self, alloc=None):
+        self._alloc = alloc or (lambda nbytes, device: torch.empty(
+            nbytes, dtype=torch.uint8, device=device))
+        self._bufs: dict[tuple, torch.Tensor] = {}
+        self._captured: set[tuple] = set()
+        self._retired: list[torch.Tensor] = []  # captured buffers outgrown
+        self._lock = threading.Lock()
+
+    def get(self, device, stream: int, nbytes: int, capturing: bool = False) -> torch.Tensor:
+        key = (str(device), int(stream))
+        need = max(int(nbytes), 256)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < need:
+                if buf is not None and key in self._captured:
+                    self._retired.append(buf)
+                self._captured.discard(key)
+                buf = self._alloc(need, device)
+                self._bufs[key] = buf
+            if capturing:
+                self._captured.add(key)
+            return buf
+
+    def cached_bytes(self) -> int:
+        """Bytes held by the live buffers (retired captured ones excluded)."""
+        return sum(b.numel() for b in self._bufs.values())
+
+    def retired_bytes(self) -> int:
+        return sum(b.numel() for b in self._retired)
+
+    def clear(self) -> None:
+        """Drop every buffer; only for callers whose graphs are all gone."""
+        with self._lock:
+            self._bufs.clear()
+            self._captured.clear()
+            self._retired.clear()
+
+
+_WS_POOL = WorkspacePool()
 
 
 def _fail(msg: str) -> None:
@@ -150,17 +202,12 @@ def _packed_cols(w: torch.Tensor) -> int:
 
 def _workspace(device: torch.device, M: int, topk: int, E: int, N: int, K: int,
                group: int, tuning: "_tuning.Tuning | None" = None) -> torch.Tensor:
-    key = (str(device), M, topk, E, N, K, group, tuning)
-    ws = _WS_CACHE.get(key)
-    if ws is None:
-        ts = None if tuning is None else tuning.to_struct()
-        nbytes = _lib.workspace_size_ex(M, topk, E, N, K, group, ts)
-        with _WS_LOCK:
-            ws = _WS_CACHE.get(key)
-            if ws is None:
-                ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-                _WS_CACHE[key] = ws
-    return ws
+    """The pool's workspace for the current stream, at least this call's size."""
+    ts = None if tuning is None else tuning.to_struct()
+    nbytes = _lib.workspace_size_ex(M, topk, E, N, K, group, ts)
+    stream = _stream_ptr(device)
+    return _WS_POOL.get(device, stream, nbytes,
+                        capturing=torch.cuda.is_current_stream_capturing())
 
 
 class _Prepared:
@@ -319,8 +366,9 @@ def fused_experts_w4a16_profiled(hidden, w1_q, w2_q, w1_scale, w2_scale, topk_we
 def workspace_tensor(hidden: torch.Tensor, topk_ids: torch.Tensor, w1_q: torch.Tensor,
                      w2_q: torch.Tensor, group_size: int = _GROUP_SIZE_DEFAULT,
                      tuning: "_tuning.Tuning | None" = None):
-    """The cached workspace fused_experts_w4a16 uses for this shape (and tuning,
-    chosen as that call chooses it), with the built-in layout's field offsets."""
+    """The workspace fused_experts_w4a16 uses for this shape on the current
+    stream (and tuning, chosen as that call chooses it), with the field
+    offsets of that call's layout."""
     M, K = hidden.shape
     topk = topk_ids.shape[1]
     E = w1_q.shape[0]
@@ -328,7 +376,8 @@ def workspace_tensor(hidden: torch.Tensor, topk_ids: torch.Tensor, w1_q: torch.T
     if tuning is None:
         tuning = _tuning.select(M, E, N, K, group_size, hidden.device)
     ws = _workspace(hidden.device, M, topk, E, N, K, group_size, tuning)
-    return ws, _lib.workspace_layout(M, topk, E, N, K, group_size)
+    ts = None if tuning is None else tuning.to_struct()
+    return ws, _lib.workspace_layout_ex(M, topk, E, N, K, group_size, ts)
 
 
 def dropped_pairs(hidden: torch.Tensor, topk_ids: torch.Tensor, w1_q: torch.Tensor,

@@ -141,8 +141,13 @@ int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts,
  * The top-k combine is summed in fp32 in slot order (deterministic).
  * Requirements: K and N multiples of 32 and of group_size, at most 16384;
  * group_size in {32, 64, 128}; 1 <= topk <= 256; 1 <= E <= 1024;
- * hidden and packed-weight pointers 16-byte aligned; ld_hidden % 8 == 0;
- * workspace 256-byte aligned and at least w4a16_moe_workspace_size bytes.
+ * M * topk < 2^30; hidden and packed-weight pointers 16-byte aligned;
+ * ld_hidden % 8 == 0; workspace 256-byte aligned and at least
+ * w4a16_moe_workspace_size bytes.  Calls that run the MFMA kernels (M above
+ * the GEMV-only bound, N and K multiples of 256) address activation rows
+ * with 32-bit byte offsets: they also need M * ld_hidden * 2 and
+ * M * topk * N * 2 at most 2^32 - 4097 bytes (W4A16_ERR_INVALID_SHAPE
+ * otherwise, before any GPU work).
  */
 int w4a16_moe_fused_experts(const void* hidden, int64_t ld_hidden,
                             const void* w13_packed, const void* w2_packed,
@@ -252,6 +257,22 @@ int w4a16_moe_default_tuning(int64_t M, int64_t topk, int64_t num_experts,
 int w4a16_moe_workspace_size_ex(int64_t M, int64_t topk, int64_t num_experts,
                                 int64_t N, int64_t K, int64_t group_size,
                                 const w4a16_moe_tuning* tuning, size_t* bytes);
+
+/* w4a16_moe_workspace_layout for calls made with `tuning` (a tuned MFMA tile
+ * height or GEMV split changes the sizes of the work lists). */
+int w4a16_moe_workspace_layout_ex(int64_t M, int64_t topk, int64_t num_experts,
+                                  int64_t N, int64_t K, int64_t group_size,
+                                  const w4a16_moe_tuning* tuning,
+                                  size_t offsets[W4A16_WS_NFIELDS]);
+
+/* Kernel launches each stage of a call with this shape and tuning enqueues:
+ * launches[4] = {expert sort, w13, w2, combine}; 0 = the stage launches
+ * nothing (e.g. no sort for self-routed decode, no combine when w2 and the
+ * top-k sum run as one kernel).  Assumes 16-byte aligned scale pointers.
+ * Measurement helper; no counterpart in the reference. */
+int w4a16_moe_stage_launches(int64_t M, int64_t topk, int64_t num_experts,
+                             int64_t N, int64_t K, int64_t group_size,
+                             const w4a16_moe_tuning* tuning, int32_t launches[4]);
 
 /* w4a16_moe_fused_experts with explicit dispatch choices: the block_m /
  * block_n / block_k arguments of fused_experts_w4a16,

@@ -170,3 +170,80 @@ def test_python_shim_rejects_without_gpu_work(pkg):
     assert pkg.is_repacked(w4) and not pkg.is_repacked(w)
     a, b = pkg.repack_weights(w, s)
     assert a is w and b is s
+
+
+def test_mfma_activation_offset_limit_is_a_shape_error(lib, pkg):
+    """Calls that run the MFMA kernels address activation rows with 32-bit
+    byte offsets; a hidden buffer past that bound is refused on the host
+    (before any GPU work) instead of failing at the kernel launch."""
+    L = pkg._lib
+    M, ld = 2048, 1 << 20  # M * ld * 2 bytes = 4 GiB
+    big = L.workspace_size(M, 10, 256, 1024, 3072, 32)
+    assert _fused(lib, M=M, ld_hidden=ld, ws_bytes=big) == L.W4A16_ERR_INVALID_SHAPE
+    # the GEMV-only path (M at most the GEMV-only bound) has 64-bit row
+    # offsets: the same stride passes the shape checks (and stops at the
+    # workspace check, still before any GPU work)
+    assert _fused(lib, M=16, ld_hidden=ld, ws_bytes=0) == L.W4A16_ERR_WORKSPACE_TOO_SMALL
+
+
+@pytest.mark.parametrize("M,want", [(0, [0, 0, 0, 0]), (1, [0, 1, 1, 0]), (4, [0, 1, 1, 0]),
+                                    (16, [0, 1, 1, 1]), (64, [1, 2, 2, 1]),
+                                    (1024, [2, 1, 1, 1]), (4096, [2, 1, 1, 1])])
+def test_stage_launches(pkg, M, want):
+    """Kernels per stage: no sort for self-routed calls (M <= 24), w2 fused
+    with the top-k sum for M <= 4, GEMV + MFMA launches for the split
+    dispatch, MFMA only once experts average 32+ pairs, the two-launch sort
+    from 8192 pairs."""
+    assert pkg._lib.stage_launches(M, 10, 256, 1024, 3072, 32, None) == want
+
+
+def test_stage_launches_follow_tuning(pkg):
+    L = pkg._lib
+    t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=0).to_struct()
+    assert L.stage_launches(16, 10, 256, 1024, 3072, 32, t) == [1, 1, 1, 1]
+    t = pkg.Tuning(w2_fused_max_m=8).to_struct()
+    assert L.stage_launches(8, 10, 256, 1024, 3072, 32, t) == [0, 1, 1, 0]
+
+
+def test_workspace_layout_ex_follows_tuning(pkg):
+    L = pkg._lib
+    args = (1024, 10, 256, 1024, 3072, 32)
+    assert L.workspace_layout_ex(*args, None) == L.workspace_layout(*args)
+    t128 = pkg.Tuning(gemv_only_max_m=24, gemv_max_tokens=4, mfma_tile_m=128).to_struct()
+    t192 = pkg.Tuning(gemv_only_max_m=24, gemv_max_tokens=4, mfma_tile_m=192).to_struct()
+    a, b = L.workspace_layout_ex(*args, t128), L.workspace_layout_ex(*args, t192)
+    # a taller MFMA tile means fewer tiles: the GEMV block list moves down
+    assert a[L.WS_TILES] == b[L.WS_TILES]
+    assert a[L.WS_GEMV_BLOCKS] > b[L.WS_GEMV_BLOCKS]
+    for off in (a, b):
+        assert all(o % 256 == 0 for o in off)
+    for t, off in ((t128, a), (t192, b)):
+        assert L.workspace_size_ex(*args, t) > max(off)
+
+
+def test_workspace_pool_holds_one_buffer_of_the_largest_need(pkg):
+    """Fifty distinct M values on one stream keep one buffer, of the largest
+    call's size; another stream gets its own; a buffer a graph captured is
+    kept (retired) when the pool grows past it."""
+    import random
+
+    import torch
+
+    L = pkg._lib
+    pool = pkg.w4a16_moe.WorkspacePool(
+        alloc=lambda n, d: torch.empty(n, dtype=torch.uint8, device="cpu"))
+    Ms = random.Random(0).sample(range(1, 5000), 50)
+    size = {M: L.workspace_size(M, 10, 256, 1024, 3072, 32) for M in Ms}
+    for M in Ms:
+        buf = pool.get("cuda:0", 7, size[M])
+        assert buf.numel() >= size[M]
+    assert pool.cached_bytes() == max(size.values())
+    assert pool.retired_bytes() == 0
+    pool.get("cuda:0", 9, size[Ms[0]])
+    assert pool.cached_bytes() == max(size.values()) + size[Ms[0]]
+    # a captured buffer outgrown by a later call stays alive
+    captured = pool.get("cuda:0", 11, 1000, capturing=True)
+    pool.get("cuda:0", 11, 5000)
+    assert pool.retired_bytes() == captured.numel() == 1000
+    pool.clear()
+    assert pool.cached_bytes() == 0 and pool.retired_bytes() == 0

@@ -40,16 +40,21 @@ def _ulp_bf16(v: torch.Tensor) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(a)) - 7)
 
 
-def mfma_experts(pkg, ti, E, N, K):
+def mfma_experts(pkg, ti, E, N, K, tuning=None):
     """Experts the fused call runs on the MFMA kernels (bf16-rounded weights).
 
-    Restates the dispatch rule of the C library: when M > GEMV_ONLY_MAX_M and
-    N and K are multiples of 256, experts with more than GEMV_MAX_TOKENS
-    routed pairs go to MFMA tiles.
+    Restates the dispatch rule of the C library: when M > gemv_only_max_m and
+    N and K are multiples of 256, experts with more than gemv_max_tokens
+    routed pairs go to MFMA tiles (the built-in values as
+    w4a16_moe_default_tuning resolves them for this M, else the tuning's).
     """
-    thr = pkg._lib.GEMV_MAX_TOKENS
     M = ti.shape[0]
-    if not (M > pkg._lib.GEMV_ONLY_MAX_M and N % 256 == 0 and K % 256 == 0):
+    if tuning is None:
+        d = pkg._lib.default_tuning(M, ti.shape[1], E, N, K, 32)
+        only, thr = d.gemv_only_max_m, d.gemv_max_tokens
+    else:
+        only, thr = tuning.gemv_only_max_m, tuning.gemv_max_tokens
+    if not (M > only and N % 256 == 0 and K % 256 == 0):
         return set()
     ids = ti.reshape(-1).cpu()
     ids = ids[(ids >= 0) & (ids < E)]
@@ -304,6 +309,24 @@ def test_one_token_w2_with_combine_bit_identical(pkg, orc, synth, dev, E, topk, 
     _check(orc, fused, x, w13, w2, s13, s2, tw, ti, group, "few-token", mismatch_max=0.03)
 
 
+@pytest.mark.parametrize("M", [5, 8])
+def test_few_token_w2_bf16_partials_bit_identical(pkg, synth, dev, M):
+    """Above M = 4 the w2 rows are rounded to bf16 before the slot sum (the
+    reference's partial buffer); the one-launch w2 + sum, when a tuning
+    extends it past M = 4, rounds them the same way and must equal the
+    separate GEMV + combine kernels bit for bit."""
+    shape = synth.LayerShape(E=256, topk=10, K=3072, N=1024, group=32)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=40 + M)
+    fused = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32,
+                                    tuning=pkg.Tuning(w2_fused_max_m=M))
+    split = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32,
+                                    tuning=pkg.Tuning(w2_fused_max_m=1))
+    torch.cuda.synchronize()
+    assert pkg._lib.stage_launches(M, 10, 256, 1024, 3072, 32,
+                                   pkg.Tuning(w2_fused_max_m=M).to_struct())[3] == 0
+    assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
+
+
 def test_dtypes_and_strides(pkg, orc, synth, dev):
     shape = synth.LayerShape(E=16, topk=4, K=512, N=256, group=32)
     M = 6
@@ -370,33 +393,34 @@ def full_layer(synth, dev):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("cfg_index", [0, 1, 2])
-def test_full_size_decode_configs(pkg, orc, synth, dev, full_layer, cfg_index):
+def _dispatch(pkg, dispatch, M, shape, dev):
+    """None for the built-in dispatch; the committed device table's entry for
+    M (the dispatch fused_experts_w4a16 and bench.py use by default)."""
+    if dispatch == "builtin":
+        return None
+    table = pkg.tuning.load_table(shape.E, shape.N, shape.K, shape.group,
+                                  pkg.tuning.device_name(dev))
+    if table is None:
+        pytest.skip("no committed tuning table for this device")
+    return pkg.tuning.nearest(table, M)
+
+
+@pytest.mark.parametrize("dispatch", ["builtin", "table"])
+@pytest.mark.parametrize("cfg_index", [0, 1, 2, 3, 4])
+def test_full_size_configs(pkg, orc, synth, dev, full_layer, cfg_index, dispatch):
+    """Every output row of every benchmark configuration at full size, under
+    the built-in dispatch and under the committed gfx950 table."""
     shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
     cfg = synth.CONFIGS[cfg_index]
-    print(f"full-size config {cfg_index}: {cfg.description}", flush=True)
+    tuning = _dispatch(pkg, dispatch, cfg.M, shape, dev)
+    print(f"full-size config {cfg_index} ({dispatch}: {tuning}): {cfg.description}", flush=True)
     x = synth.make_hidden(cfg.M, shape.K, dev, seed=0)
     tw, ti = synth.make_routing(cfg.M, shape.E, shape.topk, dev, seed=0, skewed=cfg.skewed)
-    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=tuning)
     torch.cuda.synchronize()
     _check(orc, out, x.cpu(), c13, c2, cs13, cs2, tw.cpu(), ti.cpu(), 32,
-           f"config {cfg_index}", tight=cfg.M <= 16,
-           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
-
-
-@pytest.mark.parametrize("cfg_index", [3, 4])
-def test_full_size_prefill_configs_token_sample(pkg, orc, synth, dev, full_layer, cfg_index):
-    """Rows of the output are independent per token: check a sample of them."""
-    shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
-    cfg = synth.CONFIGS[cfg_index]
-    print(f"full-size config {cfg_index}: {cfg.description}", flush=True)
-    x = synth.make_hidden(cfg.M, shape.K, dev, seed=0)
-    tw, ti = synth.make_routing(cfg.M, shape.E, shape.topk, dev, seed=0)
-    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
-    torch.cuda.synchronize()
-    rows = torch.from_numpy(np.random.default_rng(cfg_index).choice(cfg.M, 12, replace=False))
-    _check(orc, out.cpu()[rows], x.cpu()[rows], c13, c2, cs13, cs2, tw.cpu()[rows],
-           ti.cpu()[rows], 32, f"config {cfg_index} sample", tight=False)
+           f"config {cfg_index} {dispatch}",
+           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K, tuning))
 
 
 def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
