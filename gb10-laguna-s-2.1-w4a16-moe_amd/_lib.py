@@ -26,6 +26,8 @@ W4A16_ERR_INVALID_BLOCK = 6
 W4A16_ERR_HIP = 7
 W4A16_ERR_UNSUPPORTED_DTYPE = 8
 W4A16_ERR_INVALID_TUNING = 9
+W4A16_ERR_SCRATCH_TOO_SMALL = 10
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 LOGITS_F32 = 0
 LOGITS_BF16 = 1
@@ -61,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "w4a16_moe_run_stage_ex",
     "w4a16_moe_workspace_layout_ex",
     "w4a16_moe_stage_launches",
+    "w4a16_moe_fused_experts_noalloc",
     "w4a16_moe_strerror",
     "w4a16_moe_abi_version",
 )
@@ -124,6 +127,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.w4a16_moe_workspace_layout_ex.argtypes = [_i64] * 6 + [tp, ctypes.POINTER(ctypes.c_size_t)]
     lib.w4a16_moe_stage_launches.restype = ctypes.c_int
     lib.w4a16_moe_stage_launches.argtypes = [_i64] * 6 + [tp, ctypes.POINTER(ctypes.c_int32)]
+    lib.w4a16_moe_fused_experts_noalloc.restype = ctypes.c_int
+    lib.w4a16_moe_fused_experts_noalloc.argtypes = fused[:16] + [_vp, tp]
     lib.w4a16_moe_router_topk_softmax.restype = ctypes.c_int
     lib.w4a16_moe_router_topk_softmax.argtypes = [
         _vp, ctypes.c_int, _i64, _i64, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]

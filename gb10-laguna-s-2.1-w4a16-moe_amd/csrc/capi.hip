@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "../../include/w4a16_moe.h"
 #include "common.hpp"
@@ -425,6 +426,40 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   return W4A16_OK;
 }
 
+// ---- the allocation-free entry point's static scratch ----------------------
+// The workspace of w4a16_moe_fused_experts_noalloc: a file-scope device array
+// (each device holds its own copy, at its own address, until the process
+// ends).  In host code `scratch` names a host-side stand-in, never a device
+// address: the device address comes from hipGetSymbolAddress, once per device
+// with that device current, and only that pointer is handed to kernels.
+// Nothing in the workspace needs to start at zero (every call writes what it
+// reads), so the array is never cleared.
+constexpr size_t kNoallocScratchBytes = W4A16_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch's device address on `stream`'s device, which must be the
+// current device (hipGetSymbolAddress resolves the current device's copy).
+int scratch_for(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return W4A16_ERR_HIP;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) return W4A16_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return W4A16_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return W4A16_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -444,6 +479,9 @@ const char* w4a16_moe_strerror(int status) {
     case W4A16_ERR_HIP: return "HIP runtime error";
     case W4A16_ERR_UNSUPPORTED_DTYPE: return "unsupported logits dtype";
     case W4A16_ERR_INVALID_TUNING: return "invalid tuning value";
+    case W4A16_ERR_SCRATCH_TOO_SMALL:
+      return "call needs more workspace than the static scratch of the allocation-free "
+             "entry point holds";
     default: return "unknown status";
   }
 }
@@ -663,6 +701,35 @@ int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
                                 w2_scale, topk_weights, topk_ids, M, topk, num_experts, N,
                                 K, group_size, out, ld_out, workspace, workspace_bytes,
                                 stream, nullptr);
+}
+
+int w4a16_moe_fused_experts_noalloc(const void* hidden, int64_t ld_hidden,
+                                    const void* w13_packed, const void* w2_packed,
+                                    const void* w13_scale, const void* w2_scale,
+                                    const float* topk_weights, const int32_t* topk_ids,
+                                    int64_t M, int64_t topk, int64_t num_experts, int64_t N,
+                                    int64_t K, int64_t group_size, void* out, int64_t ld_out,
+                                    void* stream, const w4a16_moe_tuning* tuning) {
+  // The size check comes first: it needs no device and rejects a call too
+  // big for the scratch before anything else runs.
+  Tuning T;
+  int st = resolve_tuning(tuning, &T);
+  if (st) return st;
+  Layout L;
+  st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L);
+  if (st) return st;
+  if (M == 0) return W4A16_OK;
+  if (L.total > kNoallocScratchBytes) return W4A16_ERR_SCRATCH_TOO_SMALL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  st = scratch_for(s, &ws);
+  if (st) return st;
+  const FusedArgs a{hidden, ld_hidden, w13_packed, w2_packed, w13_scale, w2_scale,
+                    topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
+                    out, ld_out, ws, kNoallocScratchBytes, tuning};
+  st = validate(a, &L);
+  if (st) return st;
+  return run_fused(a, L, s, nullptr);
 }
 
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count, void* stream) {

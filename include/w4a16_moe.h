@@ -22,8 +22,9 @@
  *   - all GPU work is enqueued on `stream` (a hipStream_t; NULL = default
  *     stream) with no host synchronisation and no device allocation, so a
  *     call can be captured into a HIP graph (the *_profiled variant excepted);
- *   - the library holds no mutable global state; concurrent calls that share
- *     one workspace race, calls with distinct workspaces do not;
+ *   - the library holds no mutable global state (save the static scratch of
+ *     w4a16_moe_fused_experts_noalloc); concurrent calls that share one
+ *     workspace race, calls with distinct workspaces do not;
  *   - inputs are never modified.
  *
  * Expert ids outside [0, E) are not routed: the pair contributes nothing to
@@ -51,6 +52,8 @@ extern "C" {
 #define W4A16_ERR_HIP                 7  /* a HIP runtime call failed         */
 #define W4A16_ERR_UNSUPPORTED_DTYPE   8  /* router logits not fp32 or bf16    */
 #define W4A16_ERR_INVALID_TUNING      9  /* a w4a16_moe_tuning field out of range */
+#define W4A16_ERR_SCRATCH_TOO_SMALL  10  /* call too big for the static scratch of
+                                            w4a16_moe_fused_experts_noalloc    */
 
 /* Indices of w4a16_moe_workspace_layout()'s offsets array. */
 #define W4A16_WS_SORTED_IDS   0  /* int32 [EM]            sorted token-slot ids   */
@@ -195,6 +198,10 @@ int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
                             void* stream);
 
+/* ---- allocation-free variant -------------------------------------------- */
+/* Bytes of the library's static device scratch (per device). */
+#define W4A16_NOALLOC_SCRATCH_BYTES (64u << 20)
+
 /* ---- dispatch tuning (the per-M tile selector) -------------------------- */
 /*
  * How a call splits its work between the kernels.  The analogue of the
@@ -287,6 +294,32 @@ int w4a16_moe_fused_experts_ex(const void* hidden, int64_t ld_hidden,
                                void* out, int64_t ld_out, void* workspace,
                                size_t workspace_bytes, void* stream,
                                const w4a16_moe_tuning* tuning);
+
+/*
+ * w4a16_moe_fused_experts_ex with no workspace argument: the call's scratch
+ * is a static device array of W4A16_NOALLOC_SCRATCH_BYTES (64 MiB) inside
+ * the library, one per device, held until the process ends.  No counterpart
+ * in the reference: this entry point is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid allocation); it calls no hipMalloc/hipFree or allocating
+ * library routine.  The caller still passes the inputs and `out`.
+ *   - Calls whose workspace (w4a16_moe_workspace_size_ex) exceeds the scratch
+ *     return W4A16_ERR_SCRATCH_TOO_SMALL before any GPU work (at E=256,
+ *     top-10, K=3072, N=1024 the limit is M <= 818).
+ *   - `stream`'s device must be the current device.  The first call on a
+ *     device resolves the scratch's address there (outside graph capture).
+ *   - Every call on one device shares that device's scratch and keeps the
+ *     last call's contents: calls that overlap on one device (two streams,
+ *     two host threads, two graphs replayed concurrently) race.
+ */
+int w4a16_moe_fused_experts_noalloc(const void* hidden, int64_t ld_hidden,
+                                    const void* w13_packed, const void* w2_packed,
+                                    const void* w13_scale, const void* w2_scale,
+                                    const float* topk_weights, const int32_t* topk_ids,
+                                    int64_t M, int64_t topk, int64_t num_experts,
+                                    int64_t N, int64_t K, int64_t group_size,
+                                    void* out, int64_t ld_out, void* stream,
+                                    const w4a16_moe_tuning* tuning);
 
 /* w4a16_moe_run_stage with explicit dispatch choices (measurement helper). */
 int w4a16_moe_run_stage_ex(int stage, const void* hidden, int64_t ld_hidden,
