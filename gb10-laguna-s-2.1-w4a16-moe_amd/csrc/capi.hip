@@ -124,6 +124,12 @@ constexpr int64_t kAllMfmaMinPairs = 32;
 // Measured on MI355X (E=256, top-10): M=256 skewed 307 vs 406 us, M=1024
 // 505 vs 552 us; at M=4096 192 wins (1049 vs 1171 us uniform).
 constexpr int64_t kTile128MaxPairs = 64;
+// Average pairs per expert below which the built-in MFMA tile is 64 slots:
+// under skewed routing a hot expert then becomes more, shorter tiles.
+// Measured on MI355X (E=256, top-10): M=256 skewed 258 vs 323 us (tile 128)
+// and 411 us (192); uniform routing from M=64 to 512 within 1 % of the
+// other heights; M=1024 uniform 474 vs 464 us (128).
+constexpr int64_t kTile64MaxPairs = 24;
 
 int check_gemm_shape(int64_t N, int64_t K, int64_t group) {
   if (N <= 0 || K <= 0) return W4A16_ERR_INVALID_SHAPE;
@@ -156,7 +162,8 @@ int resolve_tuning(const w4a16_moe_tuning* t, Tuning* out) {
   const int tc = t->gemv_tokens_per_pass;
   if (tc != 0 && tc != 1 && tc != 2 && tc != 4) return W4A16_ERR_INVALID_TUNING;
   const int tm = t->mfma_tile_m;
-  if (tm != 0 && tm != kMfmaTileMMin && tm != kMfmaTileMMax) return W4A16_ERR_INVALID_TUNING;
+  if (tm != 0 && tm != kMfmaTileMSmall && tm != kMfmaTileMMin && tm != kMfmaTileMMax)
+    return W4A16_ERR_INVALID_TUNING;
   if (tm != 0) out->tile_m = tm;
   const int upw = t->gemv_units_per_wg;
   if (upw != 0 && upw != 1 && upw != 2 && upw != 4) return W4A16_ERR_INVALID_TUNING;
@@ -200,7 +207,9 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // pairs (more, shorter tiles: an expert's long tile is the tail of the
   // launch under skewed routing), 192 from there.
   L->tile_m = T.tile_m ? T.tile_m
-                       : ((int64_t)n_tok < kTile128MaxPairs * E ? kMfmaTileMMin : kMfmaTileMMax);
+                       : ((int64_t)n_tok < kTile64MaxPairs * E    ? kMfmaTileMSmall
+                          : (int64_t)n_tok < kTile128MaxPairs * E ? kMfmaTileMMin
+                                                                  : kMfmaTileMMax);
   L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
                         : std::min<int64_t>((int64_t)n_tok, L->nb);

@@ -96,8 +96,9 @@ __device__ __forceinline__ int wg_exclusive_scan(int v, int* wave_tot, int* tota
 namespace w4a16 {
 
 // MFMA tile: token slots x weight rows of one workgroup.  An expert's pairs
-// are cut into the fewest tiles of at most tile_m slots (128 or 192, chosen
-// per call), of near-equal size.
+// are cut into the fewest tiles of at most tile_m slots (64, 128 or 192,
+// chosen per call), of near-equal size.
+constexpr int kMfmaTileMSmall = 64;
 constexpr int kMfmaTileMMin = 128;
 constexpr int kMfmaTileMMax = 192;
 constexpr int kMfmaTileN = 256;

@@ -189,13 +189,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //      r * 128 + 16 * (c ^ g(r)), g(r) = (r ^ (r / 8)) % 8, so the lanes
 //      reading one chunk of 8 (or 16) neighbouring rows hit 8 (16) different
 //      16-byte bank groups of a 128-byte (256-byte) bank row.
-//   W  kWslots slots x 8 waves x 1 KB: a wave's packed weights of one double
-//      step, lane l's 16 bytes at l * 16.
+//   W  kWslots slots x 8 waves x 2 KB: a wave's packed weights of a pair of
+//      double steps (64 bytes of each of its 32 rows), as two DMAs of 16
+//      rows: DMA h, lane l holds row 16 h + l / 4, bytes 16 (l % 4) of the
+//      pair's 64, at h * 1024 + l * 16.
 //   S  2 slots x 8 waves x 1 KB: a wave's scales of one loop iteration (8
 //      groups of 32 elements), lane l's bytes at l times the DMA size.
 constexpr int kWaves = 8;
-constexpr int kWslots = 4;
-constexpr int kWslot = kWaves * 1024;
+constexpr int kWslots = 2;
+constexpr int kWslot = kWaves * 2048;
 constexpr int kSslot = kWaves * 1024;
 constexpr int kOffW = kAbufs * kAbuf;
 constexpr int kOffS = kOffW + kWslots * kWslot;
@@ -210,15 +212,19 @@ static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
 // hold gate and up of one output; for w2 rows 32 w ...  Two waves share each
 // SIMD: one issues MFMAs while the other waits on LDS or dequantizes.
 //
-// Every global load of the main loop is an LDS DMA, issued three double
-// steps ahead, so no vector register waits on memory there.  Issue order per
-// double step t (fixed by scheduling barriers; the prologue issues steps 0-2
-// the same way): [the next iteration's scales when t % 4 == 0] [NA
-// activation DMAs of step t + 3] [1 weight DMA of step t + 3].  At the end of
-// step t each wave waits until its weight DMA of step t + 1 (issued in step
-// t - 2, after that step's activation DMAs) has landed -- the vector-memory
-// count of the instructions behind it is exact below -- and the workgroup
-// barrier then makes every wave's activation rows visible.
+// Every global load of the main loop is an LDS DMA, issued about three
+// double steps ahead, so no vector register waits on memory there.  The
+// weights go by pairs of double steps: 64 contiguous bytes of a row per DMA
+// lane group, half the cache-line requests of per-step 32-byte pieces.
+// Issue order per double step t (fixed by scheduling barriers; the prologue
+// issues pseudo-steps -3 .. -1 the same way): [the next iteration's scales
+// when t % 4 == 0] [NA activation DMAs of step t + 3] [when t is odd: the 2
+// weight DMAs of pair (t + 3) / 2, i.e. steps t + 3 and t + 4, into the slot
+// of t's own pair, whose weights the wave has read into registers at the
+// start of t].  At the end of step t each wave waits until the last of the
+// DMAs step t + 1 needs has landed -- the vector-memory count of the
+// instructions behind it is exact below -- and the workgroup barrier then
+// makes every wave's activation rows visible.
 template <int MODE, int GSHIFT, int MC, int NA>
 __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, int nrt,
                                          const int* s_f, unsigned char* lds) {
@@ -286,26 +292,38 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // ---- the weight row of this lane ------------------------------------------
   // Row tile nt0 + rt moves every row by kTN / 2 (w13: gate and up) or kTN.
   constexpr int kRowsPerTile = MODE == 0 ? kTN / 2 : kTN;
-  int grow;
-  if (MODE == 0) {
-    const int col = nt0 * (kTN / 2) + 16 * wid + (j & 15);
-    grow = j < 16 ? col : a.n_out + col;  // gate, or the matching up row
-  } else {
-    grow = nt0 * kTN + 32 * wid + j;
-  }
+  // Weight row of local row r (0..31) of the wave's block.
+  auto wrow = [&](int r) {
+    if (MODE == 0) {
+      const int col = nt0 * (kTN / 2) + 16 * wid + (r & 15);
+      return r < 16 ? col : a.n_out + col;  // gate, or the matching up row
+    } else {
+      return nt0 * kTN + 32 * wid + r;
+    }
+  };
+  const int grow = wrow(j);
   const int64_t e_rows = (int64_t)e * rows_total;
   const char* const wexp = reinterpret_cast<const char*>(a.w) + e_rows * (kdim / 2);
   const char* const sexp = reinterpret_cast<const char*>(a.s) + e_rows * gpr * 2;
-  // 16-byte group 2t + q of the row for double step t
-  const uint32_t w_off = (uint32_t)grow * (uint32_t)(kdim / 2) + 16u * q;
+  // Weight DMA h of a pair: this lane fetches bytes 16 (lane % 4) of the
+  // pair's 64 of local row 16 h + lane / 4.
+  uint32_t w_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    w_off[h] = (uint32_t)wrow(16 * h + (lane >> 2)) * (uint32_t)(kdim / 2) + 16u * (lane & 3);
+  // Lane (j, q) reads 16-byte group 2 (t % 2) + q of row j's pair block.
+  const uint32_t w_rd = (uint32_t)((j >> 4) * 1024 + (j & 15) * 64 + q * 16);
   const uint32_t s_off = (uint32_t)grow * (uint32_t)gpr * 2u;
-  unsigned char* const w_lds = lds + kOffW + wid * 1024;  // + slot * kWslot
+  unsigned char* const w_lds = lds + kOffW + wid * 2048;  // + slot * kWslot
   unsigned char* const s_lds = lds + kOffS + wid * 1024;  // + slot * kSslot
   const uint32_t w_tile = (uint32_t)kRowsPerTile * (uint32_t)(kdim / 2);
   const uint32_t s_tile = (uint32_t)kRowsPerTile * (uint32_t)gpr * 2u;
+  // The pair of double steps k, k + 1 (k even) of row tile rt.
   auto dma_w = [&](int rt, int k, int slot) {
-    const uint32_t koff = (uint32_t)rt * w_tile + (uint32_t)k * 32u;
-    lds_dma16(wexp, w_off + koff, lds_addr(w_lds + slot * kWslot));
+    const uint32_t koff = (uint32_t)rt * w_tile + (uint32_t)(k >> 1) * 64u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      lds_dma16(wexp, w_off[h] + koff, lds_addr(w_lds + slot * kWslot + h * 1024));
   };
   // Scales of one loop iteration (8 groups of 32 elements): 16, 8 or 4 bytes
   // of the row by group size, naturally aligned (kdim % 256 == 0), as one
@@ -364,7 +382,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // The step's weight words and scale word, then its k-step 0 and 1
   // fragments (into af[0], af[1]).
   auto read_step_operands = [&](int tp, int sslot) {
-    wq = *reinterpret_cast<const u32x4_t*>(w_lds + tp * kWslot + lane * 16);
+    wq = *reinterpret_cast<const u32x4_t*>(w_lds + (tp >> 1) * kWslot + w_rd + (tp & 1) * 32);
     sw = scale_word(sslot, tp);
     read_a(lds + tp * kAbuf, 0, af[0]);
     read_a(lds + tp * kAbuf, 1, af[1]);
@@ -422,7 +440,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   };
 
   // Prologue: the scales of iteration 0, then pseudo-steps -3, -2, -1 (the
-  // DMAs of steps 0, 1, 2).
+  // activation DMAs of steps 0, 1, 2; the weights of pair 0 after step 0's,
+  // those of pair 1 after step 2's).
   dma_s(0, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -431,10 +450,10 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
     split_step(s, 0, rt, k);
     dma_a(k, s);
     __builtin_amdgcn_sched_barrier(0);
-    dma_w(rt, k, s);
+    if (s != 1) dma_w(rt, k, s >> 1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Step 0's data: behind its weight DMA are A(1), W(1), A(2), W(2).
+  // Step 0's data: behind its weights (pair 0) are A(1), A(2), W(pair 1).
   wait_vmcnt<2 * NA + 2>();
   tile_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -455,17 +474,19 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       // This step's DMAs (for step t + 3) are spread over k-steps 0-2 so that
       // the address unit drains them behind the MFMAs: [scales when tp == 0]
       // and activation DMA 0 in k-step 0, activation DMA u in k-step u, the
-      // weight DMA in k-step 2 -- still in the order the wait counts assume.
-      // Buffer and slot (t + 3) % 4 were read last for step t - 1, before the
-      // barrier of step t - 1; scale slot (it + 1) % 2 was read last for
-      // step 3 of iteration it - 1.
+      // weight DMAs (odd steps: pair (t + 3) / 2) in k-step 2 -- still in the
+      // order the wait counts assume.  Buffer (t + 3) % 4 was read last for
+      // step t - 1, before the barrier of step t - 1; weight slot
+      // (tp >> 1) & 1 holds t's own pair, whose words this wave read for t
+      // before the step began and consumed in k-step 0; scale slot
+      // (it + 1) % 2 was read last for step 3 of iteration it - 1.
       auto issue_dmas = [&](int u) {
         __builtin_amdgcn_sched_barrier(0);
         if (tp == 0 && u == 0) dma_s(it + 1, (it + 1) & 1);
 #pragma unroll
         for (int i = 0; i < NA; ++i)
           if (i == u || (u == 2 && i > 2)) dma_a1(k_d, (tp + 3) & 3, i);
-        if (u == 2) dma_w(rt_d, k_d, (tp + 3) & 3);
+        if (u == 2 && (tp & 1)) dma_w(rt_d, k_d, (tp >> 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
       };
 
@@ -506,8 +527,11 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       constexpr int kSplit = kMfmaSplit < 0 ? (MC + 1) / 2 : (kMfmaSplit > MC ? MC : kMfmaSplit);
       mfmas(3, 0, kSplit);
       __builtin_amdgcn_sched_barrier(0);
-      // Step t+1's data: behind its weight DMA (step t-2) are step t-1's
-      // [scales] A(t+2) W(t+2) and step t's [scales] A(t+3) W(t+3).
+      // Step t+1's data: its activations came in step t - 2, its weights
+      // with the last odd step at least two before t + 1.  Behind the later
+      // of the two are the DMAs of steps t - 1 and t: 2 NA activation DMAs,
+      // one weight pair (one of the two steps is odd) and the scales of the
+      // step with tp == 0 among them.
       wait_vmcnt<2 * NA + 2 + kSDmas * ((tp == 0) + (tp == 1))>();
       tile_barrier();
       __builtin_amdgcn_sched_barrier(0);

@@ -58,8 +58,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def effective(M: int, N: int, K: int, t) -> tuple:
-    """What a tuning does at M: the GEMV-only or the split dispatch."""
+def effective(M: int, N: int, K: int, t, builtin_tile: int = 192) -> tuple:
+    """What a tuning does at M: the GEMV-only or the split dispatch
+    (builtin_tile: the MFMA tile height mfma_tile_m = 0 selects at M)."""
     if M <= t.gemv_only_max_m or N % 256 or K % 256:
         fused = M <= (t.w2_fused_max_m or 4)
         return ("gemv", t.gemv_tokens_per_pass, t.gemv_units_per_wg, t.gemv_lanes_per_row,
@@ -68,7 +69,7 @@ def effective(M: int, N: int, K: int, t) -> tuple:
             t.gemv_tokens_per_pass if t.gemv_max_tokens else 0,
             t.gemv_units_per_wg if t.gemv_max_tokens else 0,
             t.gemv_lanes_per_row if t.gemv_max_tokens else 0,
-            t.mfma_tile_m or 192, t.mfma_row_tiles)
+            t.mfma_tile_m or builtin_tile, t.mfma_row_tiles)
 
 
 def candidates(M: int, N: int, K: int, Tuning, always: int, base=None):
@@ -89,11 +90,12 @@ def candidates(M: int, N: int, K: int, Tuning, always: int, base=None):
             for tc in (0, 2, 4):
                 out.append(Tuning(0, thr, tc, 0))
         out += [Tuning(0, 4, 0, 0, upw) for upw in (1, 2, 4)]
-        # MFMA token tiles of at most 128 slots (more, smaller tiles)
-        out += [Tuning(0, thr, 0, 128) for thr in (0, 4)]
+        # MFMA token tiles of at most 64 or 128 slots (more, smaller tiles)
+        out += [Tuning(0, thr, 0, tm) for thr in (0, 4) for tm in (64, 128, 192)]
+    builtin_tile = base.mfma_tile_m if base is not None and base.mfma_tile_m else 192
     seen, uniq = set(), []
     for t in out:
-        key = effective(M, N, K, t)
+        key = effective(M, N, K, t, builtin_tile)
         if key not in seen:
             seen.add(key)
             uniq.append(t)

@@ -222,9 +222,11 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *   gemv_tokens_per_pass  token rows one GEMV pass reads the weights for:
  *                         0 (the library's choice), 1, 2 or 4;
  *   mfma_tile_m           most (token, slot) pairs of one expert per MFMA
- *                         tile: 0 (the library's choice: 128 while experts
- *                         average fewer than 64 pairs, else 192), 128 or
- *                         192;
+ *                         tile: 0 (the library's choice: 64 while experts
+ *                         average fewer than 24 pairs, 128 below 64, else
+ *                         192), 64, 128 or 192 (every height computes the
+ *                         same bits: it only changes how an expert's pairs
+ *                         are split into work items);
  *   gemv_units_per_wg     64-row slabs one GEMV workgroup streams back to
  *                         back: 0 (the library's choice), 1, 2 or 4;
  *   gemv_lanes_per_row    lanes sharing one GEMV weight row: 0 (the

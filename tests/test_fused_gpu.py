@@ -458,3 +458,19 @@ def test_mfma_row_tiles_bit_identical(pkg, synth, dev, E, topk, K, N, M):
     torch.cuda.synchronize()
     for rt, o in zip((2, 3, 5, 16), outs[1:]):
         assert torch.equal(o, outs[0]), f"row tiles {rt}"
+
+
+@pytest.mark.parametrize("E,topk,K,N,M", [(8, 4, 1024, 512, 600), (256, 10, 3072, 1024, 256)])
+def test_mfma_tile_heights_bit_identical(pkg, synth, dev, E, topk, K, N, M):
+    """The tile height only changes how an expert's pairs are cut into work
+    items: every output element is accumulated in the same order, so 64-,
+    128- and 192-slot tiles give the same bits."""
+    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=32)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=23, skewed=True)
+    outs = []
+    for tm in (64, 128, 192):
+        t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=0, mfma_tile_m=tm)
+        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=t))
+    torch.cuda.synchronize()
+    for tm, o in zip((128, 192), outs[1:]):
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), f"tile {tm}"

@@ -29,7 +29,7 @@ def _fused_ex(lib, tuning, **kw):
 
 @pytest.mark.parametrize("field,value", [
     ("gemv_only_max_m", -1), ("gemv_max_tokens", -1), ("gemv_max_tokens", 16),
-    ("gemv_tokens_per_pass", 3), ("gemv_tokens_per_pass", 8), ("mfma_tile_m", 64),
+    ("gemv_tokens_per_pass", 3), ("gemv_tokens_per_pass", 8), ("mfma_tile_m", 96),
     ("mfma_tile_m", 256), ("gemv_units_per_wg", 3), ("gemv_units_per_wg", 8),
     ("gemv_lanes_per_row", 16), ("gemv_lanes_per_row", 4), ("w2_fused_max_m", -1),
     ("mfma_row_tiles", -1), ("mfma_row_tiles", 17)])
@@ -45,9 +45,12 @@ def test_default_tuning_and_workspace_sizes(pkg):
     d = L.default_tuning(16, 10, 256, 1024, 3072, 32)
     assert (d.gemv_only_max_m, d.gemv_max_tokens, d.gemv_tokens_per_pass, d.mfma_tile_m,
             d.gemv_units_per_wg, d.gemv_lanes_per_row, d.w2_fused_max_m) == \
-        (24, 4, 0, 128, 0, 0, 4)
+        (24, 4, 0, 64, 0, 0, 4)
     assert d.mfma_row_tiles == 0
-    # built-in MFMA tile height: 128 slots below 64 pairs per expert, then 192
+    # built-in MFMA tile height: 64 slots below 24 pairs per expert, 128 below
+    # 64, then 192
+    assert L.default_tuning(614, 10, 256, 1024, 3072, 32).mfma_tile_m == 64
+    assert L.default_tuning(615, 10, 256, 1024, 3072, 32).mfma_tile_m == 128
     assert L.default_tuning(1024, 10, 256, 1024, 3072, 32).mfma_tile_m == 128
     assert L.default_tuning(1638, 10, 256, 1024, 3072, 32).mfma_tile_m == 128
     assert L.default_tuning(1639, 10, 256, 1024, 3072, 32).mfma_tile_m == 192
@@ -124,6 +127,7 @@ def test_builtin_as_explicit_tuning(pkg):
     base = pkg.Tuning.from_struct(L.default_tuning(4096, 10, 256, 1024, 3072, 32))
     cands = tune.candidates(4096, 1024, 3072, pkg.Tuning, pkg.tuning.ALWAYS, base)
     assert cands[0] == base and any(c.mfma_tile_m == 128 for c in cands)
+    assert any(c.mfma_tile_m == 64 for c in cands)
 
 
 def test_candidates_are_valid(pkg):
