@@ -58,8 +58,8 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTN = kMfmaTileN;              // weight rows per tile (8 waves x 32)
 constexpr int kTMMax = kMfmaTileMMax;        // token slots per tile, at most (6 blocks of 32)
-constexpr int kAbuf = kTMMax * 128;          // one LDS activation buffer (128 B rows)
 constexpr int kAbufs = 4;                    // activation buffers (double steps in LDS)
+constexpr int kDA = kAbufs - 1;              // activation DMAs run this many steps ahead
 constexpr int kXcds = 8;
 constexpr int kStepK = 64;                   // reduction elements per double step
 constexpr int kUnroll = 4;                   // double steps per loop iteration
@@ -183,34 +183,101 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);
 }
 
+// Workgroup shapes.  NW waves (two per SIMD) of which wave w owns the
+// 32-row MFMA block w of a row tile of 32 NW weight rows, and tiles of at
+// most MCMAX token blocks of 32 slots:
+//   * NW = 8, MCMAX = 6: 256 rows x 192 slots, one workgroup per CU (144 KB of
+//     LDS), for the experts of large batches;
+//   * NW = 4, MCMAX = 2: 128 rows x 64 slots, two workgroups per CU (58 KB
+//     each), for tiles of at most 64 slots: with few pairs per expert a
+//     launch is latency-bound, and a second workgroup on the CU runs while
+//     the other waits at its barrier or on its loads, and twice as many work
+//     items spread over the CUs.
 // LDS of one workgroup (all three rings are filled by LDS DMA):
-//   A  kAbufs buffers of kTMMax rows x 128 bytes: the gathered activation
+//   A  kAbufs buffers of 32 MCMAX rows x 128 bytes: the gathered activation
 //      rows of one double step.  Chunk c (16 bytes) of row r sits at
 //      r * 128 + 16 * (c ^ g(r)), g(r) = (r ^ (r / 8)) % 8, so the lanes
 //      reading one chunk of 8 (or 16) neighbouring rows hit 8 (16) different
 //      16-byte bank groups of a 128-byte (256-byte) bank row.
-//   W  kWslots slots x 8 waves x 2 KB: a wave's packed weights of a pair of
+//   W  WSLOTS slots x NW waves x 2 KB: a wave's packed weights of a pair of
 //      double steps (64 bytes of each of its 32 rows), as two DMAs of 16
 //      rows: DMA h, lane l holds row 16 h + l / 4, bytes 16 (l % 4) of the
-//      pair's 64, at h * 1024 + l * 16.
-//   S  2 slots x 8 waves x 1 KB: a wave's scales of one loop iteration (8
-//      groups of 32 elements), lane l's bytes at l times the DMA size.
-constexpr int kWaves = 8;
-constexpr int kWslots = 2;
-constexpr int kWslot = kWaves * 2048;
-constexpr int kSslot = kWaves * 1024;
-constexpr int kOffW = kAbufs * kAbuf;
-constexpr int kOffS = kOffW + kWslots * kWslot;
-constexpr int kLdsTotal = kOffS + 2 * kSslot;
-static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
+//      pair's 64, at h * 1024 + l * 16.  The weights run 2 WSLOTS - 1 double
+//      steps ahead, deeper than the activations: they come from HBM, the
+//      activation rows mostly from L2.
+//   S  2 slots x NW waves x 512 B: a wave's scales of one loop iteration (8
+//      groups of 32 elements), lane j's bytes (lanes 0-31) at j times the
+//      DMA size.
+template <int NW, int MCMAX, int WSLOTS>
+struct TileGeo {
+  static constexpr int kWaves = NW;
+  static constexpr int kMcMax = MCMAX;
+  static constexpr int kWslots = WSLOTS;
+  static constexpr int kDW = 2 * WSLOTS - 1;     // weight DMAs run this many steps ahead
+  static constexpr int kTN = 32 * NW;            // weight rows of a row tile
+  static constexpr int kTM = 32 * MCMAX;         // token slots of a tile, at most
+  static constexpr int kAbuf = kTM * 128;        // one activation buffer
+  static constexpr int kWslot = NW * 2048;
+  static constexpr int kSslot = NW * 512;
+  static constexpr int kOffW = kAbufs * kAbuf;
+  static constexpr int kOffS = kOffW + kWslots * kWslot;
+  static constexpr int kLdsTotal = kOffS + 2 * kSslot;
+  static constexpr int kWgsPerCu = NW == 8 ? 1 : 2;
+  static_assert(kTM <= kTMMax, "tile height");
+  static_assert((kLdsTotal + kTM * 8) * kWgsPerCu <= 160 * 1024, "LDS of the workgroups of a CU");
+};
+#ifndef W4A16_MFMA_WSLOTS_BIG
+#define W4A16_MFMA_WSLOTS_BIG 2
+#endif
+#ifndef W4A16_MFMA_WSLOTS_SMALL
+#define W4A16_MFMA_WSLOTS_SMALL 2
+#endif
+using BigTile = TileGeo<8, 6, W4A16_MFMA_WSLOTS_BIG>;
+using SmallTile = TileGeo<4, 2, W4A16_MFMA_WSLOTS_SMALL>;
+
+// LDS DMAs a wave issues after the last one that double step t + 1 needs,
+// counted to the end of step t's issues.  Step s issues, in this order: the
+// scales of iteration s / 4 + 1 (s % 4 == 0, s >= 0; the prologue issues
+// those of iteration 0 first of all), NA activation DMAs for step s + kDA
+// (when s + kDA >= 0), and for odd s the two weight DMAs of the pair of
+// steps s + DW, s + DW + 1 (when s + DW >= 0); the prologue issues steps
+// -DW .. -1 the same way.  Step t + 1 needs its activations, its weight pair
+// and its iteration's scales, so the wait before it is vmcnt(dmas_behind(t)).
+constexpr int dmas_behind(int t, int NA, int DW, int KS) {
+  const int u = t + 1;
+  // its activations (step, position; a wave with NA = 0 issues none), then
+  // its weight pair, position 2, and its scales, position 0
+  int bs = NA > 0 ? u - kDA : -1000, bp = 1;
+  const int ws = 2 * (u / 2) - DW;
+  if (ws >= bs) bs = ws, bp = 2;
+  if (u >= 4) {
+    const int ss = 4 * (u / 4) - 4;
+    if (ss > bs) bs = ss, bp = 0;
+  }
+  auto acts = [&](int st) { return st + kDA >= 0 ? NA : 0; };
+  auto wts = [&](int st) { return ((st & 1) && st + DW >= 0) ? 2 : 0; };
+  int n = (bp == 0 ? acts(bs) : 0) + (bp <= 1 ? wts(bs) : 0);
+  for (int st = bs + 1; st <= t; ++st) n += (st >= 0 && st % 4 == 0 ? KS : 0) + acts(st) + wts(st);
+  return n;
+}
+// The loop waits with the count of a step far from the start, for every
+// step with the same t % 4: safe when no earlier step has fewer DMAs behind
+// its needed ones (the prologue's pseudo-steps issue fewer).
+constexpr bool steady_wait_safe(int NA, int DW, int KS) {
+  for (int t = 0; t < 32; ++t)
+    if (dmas_behind(t, NA, DW, KS) < dmas_behind(16 + t % 4, NA, DW, KS)) return false;
+  return true;
+}
+static_assert(BigTile::kTN == kTN, "row tile of the big tiles");
+static_assert(SmallTile::kTM == kMfmaTileMSmall, "small tiles are the 64-slot tiles");
 
 // One tile of MC token blocks (32 slots each).  GSHIFT = log2(group / 32).
 //
-// Wave w owns one 32-row MFMA block of the tile's 256 weight rows: for w13
-// rows 0-15 of the block are gate rows and rows 16-31 the matching up rows
-// (output columns 16 w ..), so accumulator registers r and r + 8 of a lane
-// hold gate and up of one output; for w2 rows 32 w ...  Two waves share each
-// SIMD: one issues MFMAs while the other waits on LDS or dequantizes.
+// Wave w owns one 32-row MFMA block of the row tile's 32 NW weight rows: for
+// w13 rows 0-15 of the block are gate rows and rows 16-31 the matching up
+// rows (output columns 16 w ..), so accumulator registers r and r + 8 of a
+// lane hold gate and up of one output; for w2 rows 32 w ...  Two waves share
+// each SIMD: one issues MFMAs while the other waits on LDS or dequantizes.
 //
 // Every global load of the main loop is an LDS DMA, issued about three
 // double steps ahead, so no vector register waits on memory there.  The
@@ -220,14 +287,20 @@ static_assert(kLdsTotal + kTMMax * 4 <= 160 * 1024, "LDS of one workgroup");
 // issues pseudo-steps -3 .. -1 the same way): [the next iteration's scales
 // when t % 4 == 0] [NA activation DMAs of step t + 3] [when t is odd: the 2
 // weight DMAs of pair (t + 3) / 2, i.e. steps t + 3 and t + 4, into the slot
-// of t's own pair, whose weights the wave has read into registers at the
-// start of t].  At the end of step t each wave waits until the last of the
-// DMAs step t + 1 needs has landed -- the vector-memory count of the
-// instructions behind it is exact below -- and the workgroup barrier then
-// makes every wave's activation rows visible.
-template <int MODE, int GSHIFT, int MC, int NA>
+// of t's own pair, whose words the wave has read into registers during step
+// t - 1].  In k-step 3 of step t each wave waits until the last of the DMAs
+// step t + 1 needs has landed -- the vector-memory count of the instructions
+// behind it is exact below -- and the workgroup barrier then makes every
+// wave's activation rows visible.
+template <int MODE, int GSHIFT, int MC, int NA, class G>
 __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, int nrt,
-                                         const int* s_f, unsigned char* lds) {
+                                         const int* s_f, const float* s_wt,
+                                         unsigned char* lds) {
+  constexpr int kWaves = G::kWaves;
+  constexpr int kTileN = G::kTN;
+  constexpr int kAbufG = G::kAbuf;
+  constexpr int kWslot = G::kWslot;
+  static_assert(MC >= 1 && MC <= G::kMcMax, "token blocks of a tile");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int j = lane & 31;
@@ -239,19 +312,31 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   const int IT = T / kUnroll;    // loop iterations of one row tile
   const int GT = nrt * T;        // double steps of the item (nrt row tiles)
   const int gpr = kdim / a.group;
-  // Row tile of global double step gs in [0, GT): the DMAs run up to three
-  // steps ahead, i.e. at most one row tile past rt_cur (T >= kUnroll).
+  // Row tile and local step of global double step gs (clamped to the item's
+  // last, GT - 1), from the row tile rt_cur of the current step: the DMAs
+  // run at most DW steps ahead, at most two row tiles past rt_cur (T >= 4,
+  // DW < 2 T, checked by the launcher).
   auto split_step = [&](int gs, int rt_cur, int& rt, int& k) {
     const int gc = min(gs, GT - 1);
-    rt = gc >= (rt_cur + 1) * T ? rt_cur + 1 : rt_cur;
+    rt = rt_cur + (gc >= (rt_cur + 1) * T) + (gc >= (rt_cur + 2) * T);
     k = gc - rt * T;
+  };
+  constexpr int kWslotsG = G::kWslots;
+  constexpr int DW = G::kDW;
+  static_assert(steady_wait_safe(NA, DW, GSHIFT == 1 ? 2 : 1), "DMA wait counts");
+  static_assert(dmas_behind(19, NA, DW, GSHIFT == 1 ? 2 : 1) < 64, "vmcnt range");
+  // Slot of weight pair p, from the slot of pair 2 it (wave-uniform).
+  auto wslot = [](int base, int c) {
+    int v = base + c;
+    while (v >= kWslotsG) v -= kWslotsG;
+    return v;
   };
 
   // ---- activation DMA: the tile's 4 MC DMAs of 1 KB (8 rows each) are dealt
-  // round robin over the 8 waves, so wave w issues NA = ceil((4 MC - w) / 8)
-  // of them (the caller instantiates both counts of an odd MC); DMA k fills
-  // rows 8 k .. 8 k + 7 of the buffer: lane l writes row r = 8 k + l / 8 at
-  // chunk position l % 8, so it fetches chunk (l % 8) ^ g(r) of that row.
+  // round robin over the waves, so wave w issues NA = ceil((4 MC - w) / NW)
+  // of them (the caller instantiates both counts of an uneven share); DMA k
+  // fills rows 8 k .. 8 k + 7 of the buffer: lane l writes row r = 8 k + l / 8
+  // at chunk position l % 8, so it fetches chunk (l % 8) ^ g(r) of that row.
   // Rows of padding slots read row 0.
   static_assert(NA >= 0 && NA <= (4 * MC + kWaves - 1) / kWaves, "activation DMAs per wave");
   constexpr int kNA1 = NA > 0 ? NA : 1;
@@ -272,7 +357,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // The item's row tiles share the activation rows: local step k of any.
   auto dma_a1 = [&](int k, int buf, int i) {
     const uint32_t koff = (uint32_t)k * (kStepK * 2);
-    lds_dma16(act, a_off[i] + koff, lds_addr(lds + buf * kAbuf + a_dst[i]));
+    lds_dma16(act, a_off[i] + koff, lds_addr(lds + buf * kAbufG + a_dst[i]));
   };
   auto dma_a = [&](int k, int buf) {
 #pragma unroll
@@ -290,15 +375,16 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
                                 16 * ((4 * q + u) ^ (j & 7) ^ (j >> 3) ^ (4 * par)));
 
   // ---- the weight row of this lane ------------------------------------------
-  // Row tile nt0 + rt moves every row by kTN / 2 (w13: gate and up) or kTN.
-  constexpr int kRowsPerTile = MODE == 0 ? kTN / 2 : kTN;
+  // Row tile nt0 + rt moves every row by kTileN / 2 (w13: gate and up) or
+  // kTileN.
+  constexpr int kRowsPerTile = MODE == 0 ? kTileN / 2 : kTileN;
   // Weight row of local row r (0..31) of the wave's block.
   auto wrow = [&](int r) {
     if (MODE == 0) {
-      const int col = nt0 * (kTN / 2) + 16 * wid + (r & 15);
+      const int col = nt0 * (kTileN / 2) + 16 * wid + (r & 15);
       return r < 16 ? col : a.n_out + col;  // gate, or the matching up row
     } else {
-      return nt0 * kTN + 32 * wid + r;
+      return nt0 * kTileN + 32 * wid + r;
     }
   };
   const int grow = wrow(j);
@@ -314,8 +400,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // Lane (j, q) reads 16-byte group 2 (t % 2) + q of row j's pair block.
   const uint32_t w_rd = (uint32_t)((j >> 4) * 1024 + (j & 15) * 64 + q * 16);
   const uint32_t s_off = (uint32_t)grow * (uint32_t)gpr * 2u;
-  unsigned char* const w_lds = lds + kOffW + wid * 2048;  // + slot * kWslot
-  unsigned char* const s_lds = lds + kOffS + wid * 1024;  // + slot * kSslot
+  unsigned char* const w_lds = lds + G::kOffW + wid * 2048;  // + slot * kWslot
+  unsigned char* const s_lds = lds + G::kOffS + wid * 512;   // + slot * kSslot
   const uint32_t w_tile = (uint32_t)kRowsPerTile * (uint32_t)(kdim / 2);
   const uint32_t s_tile = (uint32_t)kRowsPerTile * (uint32_t)gpr * 2u;
   // The pair of double steps k, k + 1 (k even) of row tile rt.
@@ -327,8 +413,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   };
   // Scales of one loop iteration (8 groups of 32 elements): 16, 8 or 4 bytes
   // of the row by group size, naturally aligned (kdim % 256 == 0), as one
-  // 16-byte DMA, two 4-byte DMAs or one 4-byte DMA.  Lanes q = 0 and 1 of a
-  // row load the same bytes.
+  // 16-byte DMA, two 4-byte DMAs or one 4-byte DMA, by the lanes q = 0 (the
+  // lanes q = 1 of the same rows read them from there).
   constexpr int kSBytes = GSHIFT == 0 ? 16 : 4;
   constexpr int kSDmas = GSHIFT == 1 ? 2 : 1;
   // Scales of global iteration git (clamped to the item's last).
@@ -336,20 +422,22 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
     const int gc = min(git, nrt * IT - 1);
     const int rt = gc / IT;  // once per iteration
     const uint32_t i = (uint32_t)(gc - rt * IT);
+    if (q == 0) {
 #pragma unroll
-    for (int d = 0; d < kSDmas; ++d) {
-      const uint32_t voff = s_off + (uint32_t)rt * s_tile + i * (16u >> GSHIFT) + 4u * d;
-      const uint32_t dst = lds_addr(s_lds + slot * kSslot + d * 256);
-      if constexpr (GSHIFT == 0)
-        lds_dma16(sexp, voff, dst);
-      else
-        lds_dma4(sexp, voff, dst);
+      for (int d = 0; d < kSDmas; ++d) {
+        const uint32_t voff = s_off + (uint32_t)rt * s_tile + i * (16u >> GSHIFT) + 4u * d;
+        const uint32_t dst = lds_addr(s_lds + slot * G::kSslot + d * 256);
+        if constexpr (GSHIFT == 0)
+          lds_dma16(sexp, voff, dst);
+        else
+          lds_dma4(sexp, voff, dst);
+      }
     }
   };
   // The scale word (2 bf16) holding group 2 tp + q (in units of 32
   // elements) of the iteration, and its bf16 half.
   auto scale_word = [&](int slot, int tp) {
-    const unsigned char* p = s_lds + slot * kSslot + lane * kSBytes;
+    const unsigned char* p = s_lds + slot * G::kSslot + j * kSBytes;
     if constexpr (GSHIFT == 0) return *reinterpret_cast<const uint32_t*>(p + 4 * tp);
     else if constexpr (GSHIFT == 1) return *reinterpret_cast<const uint32_t*>(p + 256 * (tp >> 1));
     else return *reinterpret_cast<const uint32_t*>(p);
@@ -363,54 +451,59 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   const Masks mk{opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
 
   f32x16_t acc[MC];
+  auto clear_acc = [&]() {
 #pragma unroll
-  for (int m = 0; m < MC; ++m)
+    for (int m = 0; m < MC; ++m)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+  };
+  clear_acc();
 
-  // Operands of a double step that are read from LDS before it starts (at
-  // the end of the previous step, behind its last MFMAs): the packed weight
-  // words, the scale word and the activation fragments of k-step 0.
-  u32x4_t wq;
-  uint32_t sw;
+  // Operands of a double step that are ready before it starts: the packed
+  // weight words and the scale of the lane's group (the wave's own DMAs, read
+  // in k-step 3 of the previous step and turned into the group constants and
+  // the k-step 0 weights there, before the barrier), and the activation
+  // fragments of k-steps 0 and 1 (read behind the barrier).
+  u32x4_t wq, wq_next;
+  uint32_t sw_next;
+  GroupScale gs;
   bf16x8_t af[4][MC], bw[2];  // af[u]: fragments of k-step u
   auto read_a = [&](const unsigned char* abuf, int u, bf16x8_t (&dst)[MC]) {
 #pragma unroll
     for (int m = 0; m < MC; ++m)
       dst[m] = *reinterpret_cast<const bf16x8_t*>(abuf + a_rd[m & 1][u] + (m >> 1) * 2 * 32 * 128);
   };
-  // The step's weight words and scale word, then its k-step 0 and 1
-  // fragments (into af[0], af[1]).
-  auto read_step_operands = [&](int tp, int sslot) {
-    wq = *reinterpret_cast<const u32x4_t*>(w_lds + (tp >> 1) * kWslot + w_rd + (tp & 1) * 32);
-    sw = scale_word(sslot, tp);
-    read_a(lds + tp * kAbuf, 0, af[0]);
-    read_a(lds + tp * kAbuf, 1, af[1]);
+  // The step's weight words (pair slot wsl) and scale word (this wave's own
+  // DMAs).
+  auto read_w_operands = [&](int tp, int wsl, int sslot) {
+    wq_next = *reinterpret_cast<const u32x4_t*>(w_lds + wsl * kWslot + w_rd + (tp & 1) * 32);
+    sw_next = scale_word(sslot, tp);
+  };
+  // Group constants and k-step 0 weights of the step whose words were read.
+  auto start_step_weights = [&](int tp) {
+    gs = group_scale(scale_value(sw_next, tp));
+    bw[0] = dequant_word(wq_next[0], gs, mk);
+    wq = wq_next;
+  };
+  // The step's k-step 0 and 1 activation fragments (into af[0], af[1]).
+  auto read_step_acts = [&](int tp) {
+    read_a(lds + tp * kAbufG, 0, af[0]);
+    read_a(lds + tp * kAbufG, 1, af[1]);
   };
 
-  // Token rows of the accumulator columns: slot 32 m + j, its routing
-  // weight (w2), loaded before the DMAs start so that no load with a register
-  // result waits behind them.
-  int f_out[MC];
-  float wt_out[MC];
-#pragma unroll
-  for (int m = 0; m < MC; ++m) {
-    f_out[m] = s_f[32 * m + j];
-    wt_out[m] = (MODE == 1 && f_out[m] < a.n_tok) ? a.topk_w[f_out[m]] : 0.0f;
-  }
-
   // Output of row tile nt.  Accumulator register r of a 32x32 block holds
-  // weight row 8 (r / 4) + 4 q + r % 4 of the wave's block and token slot j.
+  // weight row 8 (r / 4) + 4 q + r % 4 of the wave's block and token slot j;
+  // the slot's token row and routing weight (w2) are in LDS (s_f, s_wt).
   auto write_out = [&](int nt) {
 #pragma unroll
     for (int m = 0; m < MC; ++m) {
-      const int f = f_out[m];
+      const int f = s_f[32 * m + j];
       if (f >= a.n_tok) continue;
       if (MODE == 0) {
         // r < 8: gate column 8 (r / 4) + 4 q + r % 4 of the wave's 16; r + 8:
         // its up row.
         uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out +
-                        nt * (kTN / 2) + 16 * wid + 4 * q;
+                        nt * (kTileN / 2) + 16 * wid + 4 * q;
 #pragma unroll
         for (int i4 = 0; i4 < 2; ++i4) {
           float h[4];
@@ -420,8 +513,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
               u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
         }
       } else {
-        const float wt = wt_out[m];
-        const int64_t base = (int64_t)f * a.n_out + nt * kTN + 32 * wid + 4 * q;
+        const float wt = s_wt[32 * m + j];
+        const int64_t base = (int64_t)f * a.n_out + nt * kTileN + 32 * wid + 4 * q;
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
           const int64_t o = base + 8 * i4;
@@ -438,60 +531,68 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       }
     }
   };
-
-  // Prologue: the scales of iteration 0, then pseudo-steps -3, -2, -1 (the
-  // activation DMAs of steps 0, 1, 2; the weights of pair 0 after step 0's,
-  // those of pair 1 after step 2's).
+  // Prologue: the scales of iteration 0, then pseudo-steps -DW .. -1 (the
+  // activation DMAs of steps 0 .. kDA - 1, the weight pairs of steps
+  // 0 .. DW).
   dma_s(0, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int s = 0; s < 3; ++s) {
+  for (int s = -DW; s < 0; ++s) {
     int rt, k;
-    split_step(s, 0, rt, k);
-    dma_a(k, s);
+    if (s + kDA >= 0) {
+      split_step(s + kDA, 0, rt, k);
+      dma_a(k, s + kDA);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if (s != 1) dma_w(rt, k, s >> 1);
+    if ((s & 1) && s + DW >= 0) {
+      split_step(s + DW, 0, rt, k);
+      dma_w(rt, k, ((s + DW) / 2) % kWslotsG);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Step 0's data: behind its weights (pair 0) are A(1), A(2), W(pair 1).
-  wait_vmcnt<2 * NA + 2>();
+  wait_vmcnt<dmas_behind(-1, NA, DW, kSDmas)>();
+  read_w_operands(0, 0, 0);
+  start_step_weights(0);
   tile_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  read_step_operands(0, 0);
+  read_step_acts(0);
 
   // Global iterations over the item's row tiles; every IT of them finish a
   // row tile, whose outputs are written before the next one accumulates.
   // The DMA stream runs on across the row-tile boundary.
   const int n_it = nrt * IT;
   int rt_cur = 0;
+  int ws0 = 0;  // slot of weight pair 2 it
   for (int it = 0; it < n_it; ++it) {
     // One double step; tp = t % 4 is a compile-time constant.
     auto step = [&](auto tp_c) {
       constexpr int tp = decltype(tp_c)::value;
       const int t = it * kUnroll + tp;
-      int rt_d, k_d;  // row tile and local step of this step's DMAs (t + 3)
-      split_step(t + 3, rt_cur, rt_d, k_d);
-      // This step's DMAs (for step t + 3) are spread over k-steps 0-2 so that
-      // the address unit drains them behind the MFMAs: [scales when tp == 0]
-      // and activation DMA 0 in k-step 0, activation DMA u in k-step u, the
-      // weight DMAs (odd steps: pair (t + 3) / 2) in k-step 2 -- still in the
-      // order the wait counts assume.  Buffer (t + 3) % 4 was read last for
-      // step t - 1, before the barrier of step t - 1; weight slot
-      // (tp >> 1) & 1 holds t's own pair, whose words this wave read for t
-      // before the step began and consumed in k-step 0; scale slot
-      // (it + 1) % 2 was read last for step 3 of iteration it - 1.
+      int rt_a, k_a;  // row tile and local step of this step's activation DMAs
+      split_step(t + kDA, rt_cur, rt_a, k_a);
+      int rt_w = 0, k_w = 0;  // and of its weight pair (odd t)
+      if (tp & 1) split_step(t + DW, rt_cur, rt_w, k_w);
+      // This step's DMAs are spread over k-steps 0-2 so that the address
+      // unit drains them behind the MFMAs: [scales when tp == 0] and
+      // activation DMA 0 in k-step 0, activation DMA u in k-step u, the
+      // weight DMAs (odd steps: pair (t + DW) / 2) in k-step 2 -- the order
+      // dmas_behind counts.  Buffer (t + kDA) % kAbufs was read last for step
+      // t - 1, before the barrier of step t - 1; the slot of pair
+      // (t + DW) / 2 held the pair of steps t - 1 and t, whose words this
+      // wave read during steps t - 2 and t - 1; scale slot (it + 1) % 2 was
+      // read last for step 3 of iteration it - 1, during step 2.
       auto issue_dmas = [&](int u) {
         __builtin_amdgcn_sched_barrier(0);
         if (tp == 0 && u == 0) dma_s(it + 1, (it + 1) & 1);
 #pragma unroll
         for (int i = 0; i < NA; ++i)
-          if (i == u || (u == 2 && i > 2)) dma_a1(k_d, (tp + 3) & 3, i);
-        if (u == 2 && (tp & 1)) dma_w(rt_d, k_d, (tp >> 1) & 1);
+          if (i == u || (u == 2 && i > 2)) dma_a1(k_a, (tp + kDA) % kAbufs, i);
+        if (u == 2 && (tp & 1)) dma_w(rt_w, k_w, wslot(ws0, (tp + DW) / 2));
         __builtin_amdgcn_sched_barrier(0);
       };
 
-      const unsigned char* const acur = lds + tp * kAbuf;
-      GroupScale gs;
+      const unsigned char* const acur = lds + tp * kAbufG;
+      constexpr int tn = (tp + 1) & 3;
       auto mfmas = [&](int c, int m0, int m1) {
 #pragma unroll
         for (int m = m0; m < m1; ++m)
@@ -500,14 +601,10 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       // Software pipeline over the 4 MFMA k-steps u: the activation
       // fragments of u + 2 are read and the weights of u + 1 dequantized
       // while the MFMAs of u run; k-step u waits only for its own fragments
-      // (the compiler's exact LDS counts keep the reads of u + 1 in flight).
+      // (the compiler's exact LDS counts keep the later reads in flight).
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
         issue_dmas(u);
-        if (u == 0) {
-          gs = group_scale(scale_value(sw, tp));
-          bw[0] = dequant_word(wq[0], gs, mk);
-        }
         if (u < 2) read_a(acur, u + 2, af[u + 2]);
         mfmas(u, 0, MC);
         bw[(u + 1) & 1] = dequant_word(wq[u + 1], gs, mk);
@@ -520,23 +617,30 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
           __builtin_amdgcn_sched_group_barrier(0x002, (17 + MC - 1) / MC, 0);
         }
       }
-      // k-step 3: its first MFMAs, then the wait for step t+1's DMAs and the
-      // barrier, then step t+1's operand reads (into af[0], af[1]) behind the
-      // remaining MFMAs.
+      // k-step 3: the wait for step t+1's data and the wave's reads of its
+      // own weight words and scale of t+1; the first MFMAs with t+1's group
+      // constants and k-step 0 weights computed between them; the barrier
+      // (every wave's activation rows of t+1 have landed); t+1's activation
+      // reads (into af[0], af[1]) behind the remaining MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      // Step t+1's data (activations, weight pair, scales) has landed once
+      // at most dmas_behind(t) of this wave's DMAs are in flight; the count
+      // depends on t % 4 only.
+      wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
+      read_w_operands(tn, wslot(ws0, (tp + 1) / 2), tp == 3 ? ((it + 1) & 1) : (it & 1));
       __builtin_amdgcn_sched_barrier(0);
       constexpr int kSplit = kMfmaSplit < 0 ? (MC + 1) / 2 : (kMfmaSplit > MC ? MC : kMfmaSplit);
       mfmas(3, 0, kSplit);
+      start_step_weights(tn);
+#pragma unroll
+      for (int i = 0; i < kSplit; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (23 + kSplit - 1) / (kSplit > 0 ? kSplit : 1), 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
-      // Step t+1's data: its activations came in step t - 2, its weights
-      // with the last odd step at least two before t + 1.  Behind the later
-      // of the two are the DMAs of steps t - 1 and t: 2 NA activation DMAs,
-      // one weight pair (one of the two steps is odd) and the scales of the
-      // step with tp == 0 among them.
-      wait_vmcnt<2 * NA + 2 + kSDmas * ((tp == 0) + (tp == 1))>();
       tile_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      constexpr int tn = (tp + 1) & 3;
-      read_step_operands(tn, tp == 3 ? ((it + 1) & 1) : (it & 1));
+      read_step_acts(tn);
       __builtin_amdgcn_sched_barrier(0);
       mfmas(3, kSplit, MC);
     };
@@ -546,12 +650,10 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
     step(std::integral_constant<int, 3>{});
     if (it + 1 == (rt_cur + 1) * IT) {
       write_out(nt0 + rt_cur);
-#pragma unroll
-      for (int m = 0; m < MC; ++m)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[m][r] = 0.0f;
+      clear_acc();
       ++rt_cur;
     }
+    ws0 = wslot(ws0, 2);
   }
   // The reads of a step past the last (clamped DMAs, never used) are the
   // only LDS reads still in flight.
@@ -560,14 +662,17 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   wait_vmcnt<0>();
 }
 
-template <int MODE, int GSHIFT>
-__global__ __launch_bounds__(kWaves * 64, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int MODE, int GSHIFT, class G>
+__global__ __launch_bounds__(G::kWaves * 64, G::kWgsPerCu)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfma_kernel(const MfmaLaunch a) {
+  constexpr int kWaves = G::kWaves;
   extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ int s_f[kTMMax];
+  __shared__ int s_f[G::kTM];
+  __shared__ float s_wt[G::kTM];
 
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
-  const int n_tiles_n = rows_total / kTN;
+  const int n_tiles_n = rows_total / G::kTN;
   // A work item is up to row_tiles consecutive row tiles of one token tile.
   const int per_item = a.row_tiles;
   const int items_per_tile = (n_tiles_n + per_item - 1) / per_item;
@@ -586,21 +691,28 @@ void mfma_kernel(const MfmaLaunch a) {
   const int nrt = min(per_item, n_tiles_n - nt0);
   const int4 info = a.tiles[tile];
   const int e = info.x, start = info.y;
-  const int count = min(info.z, kTMMax);
+  const int count = min(info.z, G::kTM);
 
-  for (int i = threadIdx.x; i < kTMMax; i += kWaves * 64)
-    s_f[i] = i < count ? a.sorted[start + i] : a.n_tok;
+  for (int i = threadIdx.x; i < G::kTM; i += kWaves * 64) {
+    const int f = i < count ? a.sorted[start + i] : a.n_tok;
+    s_f[i] = f;
+    s_wt[i] = (MODE == 1 && f < a.n_tok) ? a.topk_w[f] : 0.0f;
+  }
   __syncthreads();
 
-  // Wave w issues ceil((4 MC - w) / 8) activation DMAs per step: for odd MC
-  // the first (4 MC) % 8 waves one more than the others.
+  // Wave w issues ceil((4 MC - w) / NW) activation DMAs per step: when NW
+  // does not divide 4 MC, the first (4 MC) % NW waves one more than the others.
   const int wid = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-#define W4A16_MFMA_TILE(MC_)                                                            \
-  case MC_:                                                                             \
-    if (wid < (4 * MC_) % kWaves)                                                       \
-      run_tile<MODE, GSHIFT, MC_, (4 * MC_ + kWaves - 1) / kWaves>(a, e, nt0, nrt, s_f, lds); \
-    else                                                                                \
-      run_tile<MODE, GSHIFT, MC_, (4 * MC_) / kWaves>(a, e, nt0, nrt, s_f, lds);        \
+#define W4A16_MFMA_TILE(MC_)                                                             \
+  case MC_:                                                                              \
+    if constexpr (MC_ <= G::kMcMax) {                                                    \
+      if (wid < (4 * MC_) % kWaves)                                                      \
+        run_tile<MODE, GSHIFT, MC_, (4 * MC_ + kWaves - 1) / kWaves, G>(a, e, nt0, nrt,  \
+                                                                       s_f, s_wt, lds);  \
+      else                                                                               \
+        run_tile<MODE, GSHIFT, MC_, (4 * MC_) / kWaves, G>(a, e, nt0, nrt, s_f, s_wt,    \
+                                                           lds);                         \
+    }                                                                                    \
     break;
   switch ((count + 31) >> 5) {
     W4A16_MFMA_TILE(1)
@@ -614,6 +726,24 @@ void mfma_kernel(const MfmaLaunch a) {
 #undef W4A16_MFMA_TILE
 }
 
+template <int MODE, class G>
+hipError_t launch_geo(const MfmaLaunch& a, hipStream_t stream) {
+  const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
+  // The DMAs run up to kDW double steps ahead, within the next two row tiles.
+  if (2 * (a.kdim / kStepK) <= G::kDW || rows_total % G::kTN != 0) return hipErrorInvalidValue;
+  const int64_t grid = (int64_t)(a.max_tiles + kXcds - 1) / kXcds * kXcds *
+                       ((rows_total / G::kTN + a.row_tiles - 1) / a.row_tiles);
+  if (grid <= 0) return hipSuccess;
+  const dim3 g((unsigned)grid), b(G::kWaves * 64);
+  switch (a.group) {
+    case 32: hipLaunchKernelGGL((mfma_kernel<MODE, 0, G>), g, b, G::kLdsTotal, stream, a); break;
+    case 64: hipLaunchKernelGGL((mfma_kernel<MODE, 1, G>), g, b, G::kLdsTotal, stream, a); break;
+    case 128: hipLaunchKernelGGL((mfma_kernel<MODE, 2, G>), g, b, G::kLdsTotal, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int MODE>
 hipError_t launch_mfma_t(const MfmaLaunch& a, hipStream_t stream) {
   const int rows_total = MODE == 0 ? 2 * a.n_out : a.n_out;
@@ -624,17 +754,10 @@ hipError_t launch_mfma_t(const MfmaLaunch& a, hipStream_t stream) {
   const int64_t act_rows = MODE == 0 ? a.n_tok / a.topk : a.n_tok;
   if (act_rows * a.ld_act * 2 > (int64_t)UINT32_MAX - 4096) return hipErrorInvalidValue;
   if (a.row_tiles < 1) return hipErrorInvalidValue;
-  const int64_t grid = (int64_t)(a.max_tiles + kXcds - 1) / kXcds * kXcds *
-                       ((rows_total / kTN + a.row_tiles - 1) / a.row_tiles);
-  if (grid <= 0) return hipSuccess;
-  const dim3 g((unsigned)grid), b(kWaves * 64);
-  switch (a.group) {
-    case 32: hipLaunchKernelGGL((mfma_kernel<MODE, 0>), g, b, kLdsTotal, stream, a); break;
-    case 64: hipLaunchKernelGGL((mfma_kernel<MODE, 1>), g, b, kLdsTotal, stream, a); break;
-    case 128: hipLaunchKernelGGL((mfma_kernel<MODE, 2>), g, b, kLdsTotal, stream, a); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  // Tiles of at most 64 slots run on 128-row workgroups, two per CU (an
+  // item is row_tiles of those row tiles).
+  if (a.tile_m <= SmallTile::kTM) return launch_geo<MODE, SmallTile>(a, stream);
+  return launch_geo<MODE, BigTile>(a, stream);
 }
 
 }  // namespace

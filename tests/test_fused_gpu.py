@@ -460,17 +460,25 @@ def test_mfma_row_tiles_bit_identical(pkg, synth, dev, E, topk, K, N, M):
         assert torch.equal(o, outs[0]), f"row tiles {rt}"
 
 
-@pytest.mark.parametrize("E,topk,K,N,M", [(8, 4, 1024, 512, 600), (256, 10, 3072, 1024, 256)])
-def test_mfma_tile_heights_bit_identical(pkg, synth, dev, E, topk, K, N, M):
+@pytest.mark.parametrize("E,topk,K,N,M,group", [(8, 4, 1024, 512, 600, 32),
+                                                (256, 10, 3072, 1024, 256, 32),
+                                                (16, 4, 256, 256, 300, 64),
+                                                (16, 4, 512, 256, 300, 128)])
+def test_mfma_tile_heights_bit_identical(pkg, orc, synth, dev, E, topk, K, N, M, group):
     """The tile height only changes how an expert's pairs are cut into work
-    items: every output element is accumulated in the same order, so 64-,
-    128- and 192-slot tiles give the same bits."""
-    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=32)
+    items (and 64-slot tiles run on the 4-wave, 128-row workgroups): every
+    output element is accumulated in the same order, so 64-, 128- and
+    192-slot tiles give the same bits, and the 64-slot result matches the
+    oracle."""
+    shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=group)
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=23, skewed=True)
     outs = []
     for tm in (64, 128, 192):
         t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=0, mfma_tile_m=tm)
-        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=t))
+        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group, tuning=t))
     torch.cuda.synchronize()
     for tm, o in zip((128, 192), outs[1:]):
         assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), f"tile {tm}"
+    if M * topk * K * N <= 1 << 31:
+        _check(orc, outs[0], x, w13, w2, s13, s2, tw, ti, group,
+               f"tile 64 E={E} K={K} N={N} G={group} M={M}", bf16_experts=set(range(E)))
