@@ -434,18 +434,31 @@ def measured_copy_bw(dev, nbytes=CALIB_BYTES, reps=5):
                     f"{reps}"}
 
 
+# L2 -> memory request counters by size: bytes = size x requests, no
+# calibration needed.  TCC_EA0_RDREQ_sum / TCC_EA0_WRREQ_sum count requests of
+# every size (reads: 32, 64 or 128 bytes; writes: 32 or 64 bytes).
+BYTE_COUNTERS = ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum",
+                 "TCC_EA0_RDREQ_sum", "TCC_EA0_WRREQ_64B_sum", "TCC_EA0_WRREQ_sum")
+
+
 def traffic_from_pmc(pmc_dirs, kernel_key):
     """HBM bytes per launch of a kernel from rocprofv3 --pmc CSV output.
 
-    pmc_dirs: directories holding *_counter_collection.csv of a FETCH_SIZE run
-    and of a WRITE_SIZE run of a command that also ran calibration_copy().
-    Each counter is scaled by CALIB_BYTES / (its reading on the copy kernel).
-    Returns (bytes, detail) or (None, reason).
+    pmc_dirs: directories holding *_counter_collection.csv of runs of this
+    command, either
+      * the request counters by size (BYTE_COUNTERS): read bytes = 32 n32 +
+        64 n64 + 128 n128, written bytes = 64 n64 + 32 (n - n64); or
+      * a FETCH_SIZE run and a WRITE_SIZE run of a command that also ran
+        calibration_copy(): each scaled by CALIB_BYTES / (its reading on the
+        copy kernel).
+    The request counters win when both are present; the calibrated figure is
+    kept in the detail for comparison.  Returns (bytes, detail) or
+    (None, reason).
     """
     import csv
     import glob
 
-    sums = {}
+    sums, req = {}, {}
     for d in pmc_dirs:
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             rows = list(csv.DictReader(open(path)))
@@ -461,11 +474,30 @@ def traffic_from_pmc(pmc_dirs, kernel_key):
                 calib_kib = max(copies)
                 factor = (CALIB_BYTES / 1024.0) / calib_kib
                 sums[name] = (sum(mine) / len(mine) * 1024.0 * factor, factor, len(mine))
-    if "FETCH_SIZE" not in sums or "WRITE_SIZE" not in sums:
-        return None, "no FETCH_SIZE/WRITE_SIZE readings for the kernel and the copy"
-    total = sums["FETCH_SIZE"][0] + sums["WRITE_SIZE"][0]
-    detail = {k: {"bytes": int(v[0]), "scale": round(v[1], 4), "dispatches": v[2]}
-              for k, v in sums.items()}
+            for name in BYTE_COUNTERS:
+                mine = [float(r["Counter_Value"]) for r in rows
+                        if r["Counter_Name"] == name and kernel_key in r["Kernel_Name"]]
+                if mine:
+                    req[name] = (sum(mine) / len(mine), len(mine))
+    detail = {}
+    total = None
+    if all(n in req for n in BYTE_COUNTERS):
+        rd = (32 * req["TCC_EA0_RDREQ_32B_sum"][0] + 64 * req["TCC_EA0_RDREQ_64B_sum"][0] +
+              128 * req["TCC_EA0_RDREQ_128B_sum"][0])
+        n64 = req["TCC_EA0_WRREQ_64B_sum"][0]
+        wr = 64 * n64 + 32 * (req["TCC_EA0_WRREQ_sum"][0] - n64)
+        total = rd + wr
+        detail["request_counters"] = {"read_bytes": int(rd), "written_bytes": int(wr),
+                                      "dispatches": req["TCC_EA0_RDREQ_sum"][1]}
+    if "FETCH_SIZE" in sums and "WRITE_SIZE" in sums:
+        calibrated = sums["FETCH_SIZE"][0] + sums["WRITE_SIZE"][0]
+        detail.update({k: {"bytes": int(v[0]), "scale": round(v[1], 4), "dispatches": v[2]}
+                       for k, v in sums.items()})
+        if total is None:
+            total = calibrated
+    if total is None:
+        return None, ("no request-counter or FETCH_SIZE/WRITE_SIZE readings for the kernel "
+                      "(and the copy)")
     return int(total), detail
 
 
@@ -545,8 +577,9 @@ def main(argv=None) -> int:
     p.add_argument("--calibrate-copy", action="store_true",
                    help=f"run one {CALIB_BYTES >> 20} MiB device copy first (PMC calibration)")
     p.add_argument("--pmc-dir", action="append", default=[],
-                   help="rocprofv3 --pmc output dirs (FETCH_SIZE and WRITE_SIZE runs of this "
-                        "command with --calibrate-copy) to derive roofline.traffic from")
+                   help="rocprofv3 --pmc output dirs of this command (request counters "
+                        "TCC_EA0_RDREQ_*/WRREQ_*, or FETCH_SIZE and WRITE_SIZE with "
+                        "--calibrate-copy) to derive roofline.traffic from")
     args = p.parse_args(argv)
 
     if args.gpus != 1:

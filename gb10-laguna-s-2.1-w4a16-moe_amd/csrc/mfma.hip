@@ -664,7 +664,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
 
 template <int MODE, int GSHIFT, class G>
 __global__ __launch_bounds__(G::kWaves * 64, G::kWgsPerCu)
-__attribute__((amdgpu_waves_per_eu(2, 2)))
+__attribute__((amdgpu_waves_per_eu(G::kWgsPerCu * G::kWaves / 4, G::kWgsPerCu * G::kWaves / 4)))
 void mfma_kernel(const MfmaLaunch a) {
   constexpr int kWaves = G::kWaves;
   extern __shared__ __align__(16) unsigned char lds[];
