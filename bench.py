@@ -434,6 +434,44 @@ def measured_copy_bw(dev, nbytes=CALIB_BYTES, reps=5):
                     f"{reps}"}
 
 
+def measured_dense_gemm(dev, m=40960, n=2048, k=3072, warm_ms=300.0, reps=20):
+    """A plain bf16 GEMM (torch.matmul, hipBLASLt) with the w13 launch's FLOPs
+    at configs[4] (M*topk rows, 2N columns, K deep), run back to back for
+    warm_ms first so the board reaches the clock it sustains under MFMA load;
+    p50 of reps timed calls.  The library's dense rate at that clock, reported
+    beside the 2.5 PFLOP/s nominal peak."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn(m, k, device=dev, dtype=torch.bfloat16, generator=g)
+    b = torch.randn(k, n, device=dev, dtype=torch.bfloat16, generator=g)
+    c = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(10):
+            torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        torch.matmul(a, b, out=c)
+        en.record()
+        torch.cuda.synchronize()
+        times.append(st.elapsed_time(en) * 1e-3)
+    del a, b, c
+    torch.cuda.empty_cache()
+    p50 = sorted(times)[len(times) // 2]
+    flop = 2.0 * m * n * k
+    return {"TFLOP_s": round(flop / p50 / 1e12, 1), "us_per_gemm": round(p50 * 1e6, 2),
+            "frac_of_peak": round(flop / p50 / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "shape": [m, n, k],
+            "note": "torch.matmul bf16 (hipBLASLt), the w13 FLOPs of configs[4] as one dense "
+                    f"GEMM, p50 of {reps} after {warm_ms:.0f} ms of back-to-back calls"}
+
+
 # L2 -> memory request counters by size: bytes = size x requests, no
 # calibration needed.  TCC_EA0_RDREQ_sum / TCC_EA0_WRREQ_sum count requests of
 # every size (reads: 32, 64 or 128 bytes; writes: 32 or 64 bytes).
@@ -574,6 +612,8 @@ def main(argv=None) -> int:
     p.add_argument("--no-parity", action="store_true",
                    help="skip the per-config oracle comparison and CPU timing")
     p.add_argument("--stage-replays", type=int, default=8)
+    p.add_argument("--no-dense-gemm", action="store_true",
+                   help="skip the hipBLASLt dense bf16 GEMM reported beside the MFMA peak")
     p.add_argument("--calibrate-copy", action="store_true",
                    help=f"run one {CALIB_BYTES >> 20} MiB device copy first (PMC calibration)")
     p.add_argument("--pmc-dir", action="append", default=[],
@@ -664,6 +704,9 @@ def main(argv=None) -> int:
 
     copy_bw = measured_copy_bw(dev)
     log(f"measured device copy: {copy_bw['GB_s']} GB/s")
+    dense = None if args.no_dense_gemm else measured_dense_gemm(dev)
+    if dense:
+        log(f"measured dense bf16 GEMM: {json.dumps(dense)}")
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
@@ -703,6 +746,7 @@ def main(argv=None) -> int:
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline,
         "hbm_copy_measured": copy_bw,
+        "mfma_dense_measured": dense,
         "cpu_baseline": cpu,
         "configs": sweep,
     }

@@ -85,6 +85,13 @@ constexpr int kW2FusedMaxM = 4;
 // most this many tokens, which accumulate them in fp32 (:763).  The partial
 // rows here follow the same rounding points.
 constexpr int64_t kFp32PartialMaxM = 4;
+// The split dispatch runs each GEMM's GEMV and MFMA work items as one mixed
+// launch where a mixed kernel covers the shapes (0: always two launches;
+// overridable at build time for measurements).
+#ifndef W4A16_MIXED_LAUNCHES
+#define W4A16_MIXED_LAUNCHES 1
+#endif
+constexpr bool kMixedLaunches = W4A16_MIXED_LAUNCHES != 0;
 // Row tiles (256 weight rows) one MFMA workgroup runs in turn for one token
 // tile (a work item): the loads stream on across them, so the latency of a
 // workgroup's first loads is paid once per item, at the price of fewer and
@@ -293,56 +300,42 @@ int validate(const FusedArgs& a, Layout* L) {
   return W4A16_OK;
 }
 
-// Launch the four stages (or only stage `only` when it is 0..3); `ev`
-// (5 events or null) brackets them.
-int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_t* ev,
-              int only = -1) {
-  auto want = [only](int stage) { return only < 0 || only == stage; };
-  char* ws = static_cast<char*>(a.ws);
-  int32_t* header = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_HEADER]);
-  int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_SORTED_IDS]);
-  int32_t* eids = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_EXPERT_IDS]);
-  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_OFFSETS]);
-  uint16_t* inter = reinterpret_cast<uint16_t*>(ws + L.off[W4A16_WS_INTER]);
-  void* partial = ws + L.off[W4A16_WS_PARTIAL];
-  const int32_t n_tok = (int32_t)(a.M * a.topk);
+// Workspace pointers of one call.
+struct Work {
+  int32_t* header;
+  int32_t* sorted;
+  int32_t* eids;
+  int32_t* offsets;
+  uint16_t* inter;
+  void* partial;
+  int4* tiles;
+  int32_t* gemv_blocks;
+  int32_t* chunks;
+};
 
-  (void)hipGetLastError();
-  if (ev && hipEventRecord(ev[0], stream) != hipSuccess) return W4A16_ERR_HIP;
+Work work_of(const Layout& L, void* ws_base) {
+  char* ws = static_cast<char*>(ws_base);
+  Work w;
+  w.header = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_HEADER]);
+  w.sorted = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_SORTED_IDS]);
+  w.eids = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_EXPERT_IDS]);
+  w.offsets = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_OFFSETS]);
+  w.inter = reinterpret_cast<uint16_t*>(ws + L.off[W4A16_WS_INTER]);
+  w.partial = ws + L.off[W4A16_WS_PARTIAL];
+  w.tiles = reinterpret_cast<int4*>(ws + L.off[W4A16_WS_TILES]);
+  w.gemv_blocks = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_GEMV_BLOCKS]);
+  w.chunks = L.chunked ? reinterpret_cast<int32_t*>(ws + L.off_chunks) : nullptr;
+  return w;
+}
 
-  int4* tiles = reinterpret_cast<int4*>(ws + L.off[W4A16_WS_TILES]);
-  int32_t* gemv_blocks = reinterpret_cast<int32_t*>(ws + L.off[W4A16_WS_GEMV_BLOCKS]);
-
-  AlignLaunch al{};
-  al.ids = a.ids;
-  al.n_tok = n_tok;
-  al.num_experts = (int32_t)a.E;
-  al.block = W4A16_FUSED_BLOCK_M;
-  al.em = (int32_t)L.em;
-  al.n_blocks = (int32_t)L.nb;
-  al.sorted = sorted;
-  al.expert_ids = eids;
-  al.num_post = header;
-  al.offsets = offsets;
-  al.dropped = header + 1;
-  al.chunk_scratch = L.chunked ? reinterpret_cast<int32_t*>(ws + L.off_chunks) : nullptr;
-  if (L.mfma) {
-    al.tiles = tiles;
-    al.n_tiles = header + 2;
-    al.gemv_blocks = gemv_blocks;
-    al.n_gemv = header + 3;
-    al.gemv_max_tokens = L.gemv_max_tokens;
-    al.tile_m = L.tile_m;
-  }
-  if (want(0) && !L.route && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
-  if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
-
+// The GEMV launch of GEMM `mode` (0: w13, 1: w2).
+GemvLaunch gemv_args(const FusedArgs& a, const Layout& L, const Work& w, int mode) {
   GemvLaunch g{};
-  g.block_list = L.mfma ? gemv_blocks : nullptr;
-  g.sorted = sorted;
-  g.expert_ids = eids;
-  g.header = header;
-  g.n_tok = n_tok;
+  g.block_list = L.mfma ? w.gemv_blocks : nullptr;
+  g.sorted = w.sorted;
+  g.expert_ids = w.eids;
+  g.header = w.header;
+  g.n_tok = (int32_t)(a.M * a.topk);
   g.topk = (int32_t)a.topk;
   g.block = W4A16_FUSED_BLOCK_M;
   g.group = (int32_t)a.group;
@@ -354,74 +347,142 @@ int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_
   if (L.route) {
     g.ids = a.ids;
     g.max_items = (int32_t)L.max_items;
-    g.dropped_out = header + 1;
+    g.dropped_out = w.header + 1;
   }
+  if (mode == 0) {
+    g.act = static_cast<const uint16_t*>(a.hidden);
+    g.ld_act = a.ld_hidden;
+    g.w = static_cast<const uint32_t*>(a.w13);
+    g.s = static_cast<const uint16_t*>(a.s13);
+    g.topk_w = nullptr;
+    g.out = w.inter;
+    g.n_out = (int32_t)a.N;
+    g.kdim = (int32_t)a.K;
+  } else {
+    g.act = w.inter;
+    g.ld_act = a.N;
+    g.w = static_cast<const uint32_t*>(a.w2);
+    g.s = static_cast<const uint16_t*>(a.s2);
+    g.topk_w = a.topk_w;
+    g.out = w.partial;
+    g.partial_bf16 = L.partial_bf16;
+    g.n_out = (int32_t)a.K;
+    g.kdim = (int32_t)a.N;
+  }
+  return g;
+}
 
-  g.act = static_cast<const uint16_t*>(a.hidden);
-  g.ld_act = a.ld_hidden;
-  g.w = static_cast<const uint32_t*>(a.w13);
-  g.s = static_cast<const uint16_t*>(a.s13);
-  g.topk_w = nullptr;
-  g.out = inter;
-  g.n_out = (int32_t)a.N;
-  g.kdim = (int32_t)a.K;
+// The MFMA launch of GEMM `mode`.
+MfmaLaunch mfma_args(const FusedArgs& a, const Layout& L, const Work& w, int mode) {
   MfmaLaunch m{};
-  m.sorted = sorted;
-  m.tiles = tiles;
-  m.header = header;
-  m.n_tok = n_tok;
+  m.sorted = w.sorted;
+  m.tiles = w.tiles;
+  m.header = w.header;
+  m.n_tok = (int32_t)(a.M * a.topk);
   m.topk = (int32_t)a.topk;
   m.group = (int32_t)a.group;
   m.max_tiles = (int32_t)L.max_tiles;
   m.tile_m = L.tile_m;
-
-  if (want(1) && L.gemv && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
-  if (L.mfma && want(1)) {
-    m.act = g.act;
-    m.ld_act = g.ld_act;
-    m.w = g.w;
-    m.s = g.s;
+  if (mode == 0) {
+    m.act = static_cast<const uint16_t*>(a.hidden);
+    m.ld_act = a.ld_hidden;
+    m.w = static_cast<const uint32_t*>(a.w13);
+    m.s = static_cast<const uint16_t*>(a.s13);
     m.topk_w = nullptr;
-    m.out = inter;
+    m.out = w.inter;
     m.n_out = (int32_t)a.N;
     m.kdim = (int32_t)a.K;
     m.row_tiles = L.row_tiles_w13;
-    if (launch_w13_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
-  }
-  if (ev && hipEventRecord(ev[2], stream) != hipSuccess) return W4A16_ERR_HIP;
-
-  g.act = inter;
-  g.ld_act = a.N;
-  g.w = static_cast<const uint32_t*>(a.w2);
-  g.s = static_cast<const uint16_t*>(a.s2);
-  g.topk_w = a.topk_w;
-  g.out = partial;
-  g.partial_bf16 = L.partial_bf16;
-  g.n_out = (int32_t)a.K;
-  g.kdim = (int32_t)a.N;
-  if (want(2)) {
-    const hipError_t st =
-        L.token ? launch_w2_token(g, static_cast<uint16_t*>(a.out), a.ld_out, stream)
-                : (L.gemv ? launch_w2_gemv(g, stream) : hipSuccess);
-    if (st != hipSuccess) return W4A16_ERR_HIP;
-  }
-  if (L.mfma && want(2)) {
-    m.act = inter;
+  } else {
+    m.act = w.inter;
     m.ld_act = a.N;
-    m.w = g.w;
-    m.s = g.s;
+    m.w = static_cast<const uint32_t*>(a.w2);
+    m.s = static_cast<const uint16_t*>(a.s2);
     m.topk_w = a.topk_w;
-    m.out = partial;
+    m.out = w.partial;
     m.partial_bf16 = L.partial_bf16;
     m.n_out = (int32_t)a.K;
     m.kdim = (int32_t)a.N;
     m.row_tiles = L.row_tiles_w2;
-    if (launch_w2_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
+  }
+  return m;
+}
+
+// Whether GEMM `mode` of the split dispatch (GEMV and MFMA work items both)
+// runs as one mixed launch.
+bool mixed_launch(const FusedArgs& a, const Layout& L, const Work& w, int mode) {
+  return kMixedLaunches && L.gemv && L.mfma && !L.route &&
+         mixed_fits(mode, mfma_args(a, L, w, mode), gemv_args(a, L, w, mode));
+}
+
+// Launch the four stages (or only stage `only` when it is 0..3); `ev`
+// (5 events or null) brackets them.
+int run_fused(const FusedArgs& a, const Layout& L, hipStream_t stream, hipEvent_t* ev,
+              int only = -1) {
+  auto want = [only](int stage) { return only < 0 || only == stage; };
+  const Work w = work_of(L, a.ws);
+  const int32_t n_tok = (int32_t)(a.M * a.topk);
+
+  (void)hipGetLastError();
+  if (ev && hipEventRecord(ev[0], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  AlignLaunch al{};
+  al.ids = a.ids;
+  al.n_tok = n_tok;
+  al.num_experts = (int32_t)a.E;
+  al.block = W4A16_FUSED_BLOCK_M;
+  al.em = (int32_t)L.em;
+  al.n_blocks = (int32_t)L.nb;
+  al.sorted = w.sorted;
+  al.expert_ids = w.eids;
+  al.num_post = w.header;
+  al.offsets = w.offsets;
+  al.dropped = w.header + 1;
+  al.chunk_scratch = w.chunks;
+  if (L.mfma) {
+    al.tiles = w.tiles;
+    al.n_tiles = w.header + 2;
+    al.gemv_blocks = w.gemv_blocks;
+    al.n_gemv = w.header + 3;
+    al.gemv_max_tokens = L.gemv_max_tokens;
+    al.tile_m = L.tile_m;
+  }
+  if (want(0) && !L.route && launch_align(al, stream) != hipSuccess) return W4A16_ERR_HIP;
+  if (ev && hipEventRecord(ev[1], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  // w13 (+ SiLU * up): GEMV and/or MFMA work items, in one launch where the
+  // split dispatch has a mixed kernel for the shapes.
+  if (want(1)) {
+    const GemvLaunch g = gemv_args(a, L, w, 0);
+    const MfmaLaunch m = mfma_args(a, L, w, 0);
+    if (mixed_launch(a, L, w, 0)) {
+      if (launch_w13_mixed(m, g, stream) != hipSuccess) return W4A16_ERR_HIP;
+    } else {
+      if (L.gemv && launch_w13_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+      if (L.mfma && launch_w13_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
+    }
+  }
+  if (ev && hipEventRecord(ev[2], stream) != hipSuccess) return W4A16_ERR_HIP;
+
+  // w2 (x routing weight): the one-launch w2 + top-k sum of few-token calls,
+  // else GEMV and/or MFMA work items writing partial rows.
+  if (want(2)) {
+    const GemvLaunch g = gemv_args(a, L, w, 1);
+    const MfmaLaunch m = mfma_args(a, L, w, 1);
+    if (L.token) {
+      if (launch_w2_token(g, static_cast<uint16_t*>(a.out), a.ld_out, stream) != hipSuccess)
+        return W4A16_ERR_HIP;
+    } else if (mixed_launch(a, L, w, 1)) {
+      if (launch_w2_mixed(m, g, stream) != hipSuccess) return W4A16_ERR_HIP;
+    } else {
+      if (L.gemv && launch_w2_gemv(g, stream) != hipSuccess) return W4A16_ERR_HIP;
+      if (L.mfma && launch_w2_mfma(m, stream) != hipSuccess) return W4A16_ERR_HIP;
+    }
   }
   if (ev && hipEventRecord(ev[3], stream) != hipSuccess) return W4A16_ERR_HIP;
 
   CombineLaunch c{};
-  c.partial = partial;
+  c.partial = w.partial;
   c.partial_bf16 = L.partial_bf16;
   c.ids = a.ids;
   c.out = static_cast<uint16_t*>(a.out);
@@ -607,9 +668,20 @@ int w4a16_moe_stage_launches(int64_t M, int64_t topk, int64_t num_experts, int64
   if (M == 0) return W4A16_OK;
   // The same decisions as run_fused (scales assumed 16-byte aligned, as
   // torch allocations are).
+  // Stand-in pointers, suitably aligned: only the mixed-launch decision
+  // reads them (scale alignment).
+  alignas(256) static const unsigned char stand_in[256] = {};
+  const void* p = stand_in;
+  const FusedArgs a{p, K, p, p, p, p, reinterpret_cast<const float*>(p),
+                    reinterpret_cast<const int32_t*>(p), M, topk, num_experts, N, K,
+                    group_size, const_cast<void*>(p), K, const_cast<void*>(p), L.total, tuning};
+  const Work w = work_of(L, const_cast<void*>(p));
+  auto gemm = [&](int mode) {
+    return mixed_launch(a, L, w, mode) ? 1 : (L.gemv ? 1 : 0) + (L.mfma ? 1 : 0);
+  };
   launches[0] = L.route ? 0 : (L.chunked ? 2 : 1);
-  launches[1] = (L.gemv ? 1 : 0) + (L.mfma ? 1 : 0);
-  launches[2] = L.token ? 1 : (L.gemv ? 1 : 0) + (L.mfma ? 1 : 0);
+  launches[1] = gemm(0);
+  launches[2] = L.token ? 1 : gemm(1);
   launches[3] = L.token ? 0 : 1;
   return W4A16_OK;
 }

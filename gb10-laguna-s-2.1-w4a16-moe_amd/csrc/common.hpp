@@ -208,6 +208,15 @@ struct MfmaLaunch {
 hipError_t launch_w13_mfma(const MfmaLaunch& a, hipStream_t stream);
 hipError_t launch_w2_mfma(const MfmaLaunch& a, hipStream_t stream);
 
+// The split dispatch's GEMV and MFMA work items of one GEMM (mode 0: w13,
+// 1: w2) in one launch, when mixed_fits(mode, m, g): m and g are the two
+// launches' arguments.  The 128-row MFMA geometry (tiles of at most 64
+// slots), 8-lane GEMV rows with 2 or 4 token rows per pass, one row slab per
+// workgroup and the unrolled step loop of K = 3072 (w13) / N = 1024 (w2).
+bool mixed_fits(int mode, const MfmaLaunch& m, const GemvLaunch& g);
+hipError_t launch_w13_mixed(const MfmaLaunch& m, const GemvLaunch& g, hipStream_t stream);
+hipError_t launch_w2_mixed(const MfmaLaunch& m, const GemvLaunch& g, hipStream_t stream);
+
 struct CombineLaunch {
   const void* partial;     // [M*topk, K], bf16 or fp32
   int32_t partial_bf16;

@@ -187,13 +187,13 @@ def test_mfma_activation_offset_limit_is_a_shape_error(lib, pkg):
 
 
 @pytest.mark.parametrize("M,want", [(0, [0, 0, 0, 0]), (1, [0, 1, 1, 0]), (4, [0, 1, 1, 0]),
-                                    (16, [0, 1, 1, 1]), (64, [1, 2, 2, 1]),
+                                    (16, [0, 1, 1, 1]), (64, [1, 1, 1, 1]),
                                     (1024, [2, 1, 1, 1]), (4096, [2, 1, 1, 1])])
 def test_stage_launches(pkg, M, want):
     """Kernels per stage: no sort for self-routed calls (M <= 24), w2 fused
-    with the top-k sum for M <= 4, GEMV + MFMA launches for the split
-    dispatch, MFMA only once experts average 32+ pairs, the two-launch sort
-    from 8192 pairs."""
+    with the top-k sum for M <= 4, one mixed GEMV + MFMA launch per GEMM for
+    the split dispatch, MFMA only once experts average 32+ pairs, the
+    two-launch sort from 8192 pairs."""
     assert pkg._lib.stage_launches(M, 10, 256, 1024, 3072, 32, None) == want
 
 
