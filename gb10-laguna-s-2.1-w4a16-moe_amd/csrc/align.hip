@@ -361,7 +361,6 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   __shared__ int32_t wl_tot[(kTileClasses + 1) * 17];
   constexpr int nw = kChunkWaves;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
   const int wid = tid >> 6;
   const int E = a.num_experts;
   const int B = a.block;

@@ -24,10 +24,10 @@ void gemv_kernel(const GemvLaunch a) {
 
 // The w2 GEMV and the top-k combine of a few-token call in one launch.
 //
-// A workgroup has one wave per slot (topk <= 16) and owns 8 output rows of
+// A workgroup has one wave per slot (topk <= 16) and owns 8 R output rows of
 // one token (blockIdx.y); an expert routed from several tokens is read once
 // per token.
-// Wave t computes slot t's 8 rows exactly as gemv_kernel<1, ...> does (8
+// Wave t computes slot t's 8 R rows exactly as gemv_kernel<1, ...> does (8
 // lanes per row on groups 8*it + lane%8, the same dot2 chain per word and
 // fma per group, the same 8-lane sum), multiplies by the routing weight and
 // parks the value in LDS.  The workgroup then adds the slots in order from
@@ -36,7 +36,7 @@ void gemv_kernel(const GemvLaunch a) {
 // bf16 rounding of each weighted slot value when the call keeps bf16 partial
 // rows), with one launch, no partial rows in memory, and every wave's weight
 // loads in flight at once.
-template <int NIT>
+template <int NIT, int R>
 __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint16_t* out,
                                                        int64_t ld_out) {
   extern __shared__ u32x4_t lds[];
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
   const int row_oct = staged_row_octets(kdim);
   u32x4_t* xp = lds + t * row_oct;
   float* xc = reinterpret_cast<float*>(lds + topk * row_oct) + t * (G + 1);
-  float* red = reinterpret_cast<float*>(lds + topk * row_oct) + topk * (G + 1);  // [topk][8]
+  float* red = reinterpret_cast<float*>(lds + topk * row_oct) + topk * (G + 1);  // [topk][8R]
 
   const int E = a.num_experts;
   const int e_raw = a.ids[f];
@@ -61,31 +61,34 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
   const int e = valid ? e_raw : 0;
   stage_row<64>(a.act + (int64_t)f * a.ld_act, kdim, xp, xc, lane);
 
+  // Lane (r, sl) owns rows rb0 + r + 8 j, j < R, of the workgroup's 8 R.
   const int r = lane >> 3, sl = lane & 7;
-  const int row = blockIdx.x * 8 + r;
-  const char* wrow = reinterpret_cast<const char*>(a.w) + ((int64_t)e * a.n_out + row) * G * 16;
-  const char* srow = reinterpret_cast<const char*>(a.s) + ((int64_t)e * a.n_out + row) * gpr * 2;
+  const int rb0 = blockIdx.x * 8 * R;
+  const char* wrow = reinterpret_cast<const char*>(a.w) + ((int64_t)e * a.n_out + rb0 + r) * G * 16;
+  const char* srow = reinterpret_cast<const char*>(a.s) + ((int64_t)e * a.n_out + rb0 + r) * gpr * 2;
+  const int64_t wstep = (int64_t)8 * G * 16, sstep = (int64_t)8 * gpr * 2;  // 8 rows on
   const uint32_t mask = a.nib_mask;
   uint32_t magic;
   asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.nib_magic));
   const int n_it = NIT > 0 ? NIT : (G + 7) >> 3;
   constexpr int kMaxIt = NIT > 0 ? NIT : 1;
 
-  // All loads first (NIT of them), then the staged row is ready.
-  u32x4_t wq[kMaxIt];
-  uint32_t sq[kMaxIt];
+  // All loads first (NIT x R of them), then the staged row is ready.
+  u32x4_t wq[R][kMaxIt];
+  uint32_t sq[R][kMaxIt];
   if constexpr (NIT > 0) {
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int gi = min(it * 8 + sl, G - 1);
-      wq[it] = *reinterpret_cast<const u32x4_t*>(wrow + gi * 16);
-      sq[it] = *reinterpret_cast<const uint16_t*>(srow + (gi >> gshift) * 2);
-    }
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int gi = min(it * 8 + sl, G - 1);
+        wq[j][it] = *reinterpret_cast<const u32x4_t*>(wrow + j * wstep + gi * 16);
+        sq[j][it] = *reinterpret_cast<const uint16_t*>(srow + j * sstep + (gi >> gshift) * 2);
+      }
   }
   __syncthreads();
 
-  float acc = 0.0f;
-  auto step = [&](const u32x4_t& w4, uint32_t sbits, int it) {
+  auto step = [&](const u32x4_t& w4, uint32_t sbits, int it, float& acc) {
     const int gi = it * 8 + sl;
     const int gl = gi < G ? gi : G;
     float pj = xc[gl];  // -C
@@ -104,39 +107,55 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
     }
     acc = fmaf(bf16_to_f32(sbits), pj, acc);
   };
-  if constexpr (NIT > 0) {
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) step(wq[it], sq[it], it);
-  } else {
-    for (int it = 0; it < n_it; ++it) {
-      const int gi = min(it * 8 + sl, G - 1);
-      const u32x4_t w4 = *reinterpret_cast<const u32x4_t*>(wrow + gi * 16);
-      const uint32_t sb = *reinterpret_cast<const uint16_t*>(srow + (gi >> gshift) * 2);
-      step(w4, sb, it);
+  for (int j = 0; j < R; ++j) {
+    float acc = 0.0f;
+    if constexpr (NIT > 0) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) step(wq[j][it], sq[j][it], it, acc);
+    } else {
+      for (int it = 0; it < n_it; ++it) {
+        const int gi = min(it * 8 + sl, G - 1);
+        const u32x4_t w4 = *reinterpret_cast<const u32x4_t*>(wrow + j * wstep + gi * 16);
+        const uint32_t sb =
+            *reinterpret_cast<const uint16_t*>(srow + j * sstep + (gi >> gshift) * 2);
+        step(w4, sb, it, acc);
+      }
     }
+    acc = oct_sum(acc);
+    // The weighted slot value is rounded to bf16 when the call keeps bf16
+    // partial rows (M > 4), as gemv_kernel<1> stores it for combine_kernel.
+    float v = acc * wt;
+    if (a.partial_bf16) v = bf16_to_f32(f32_to_bf16(v));
+    // A slot routed outside [0, E) parks +0.0: the sum starts at +0.0 and so
+    // is never -0.0, and adding +0.0 to any other value leaves it unchanged,
+    // so summing every slot equals skipping those -- without reading the ids
+    // again here.
+    if (sl == 0) red[t * 8 * R + r + 8 * j] = valid ? v : 0.0f;
   }
-  acc = oct_sum(acc);
-  // The weighted slot value is rounded to bf16 when the call keeps bf16
-  // partial rows (M > 4), as gemv_kernel<1> stores it for combine_kernel.
-  float v = acc * wt;
-  if (a.partial_bf16) v = bf16_to_f32(f32_to_bf16(v));
-  // A slot routed outside [0, E) parks +0.0: the sum starts at +0.0 and so
-  // is never -0.0, and adding +0.0 to any other value leaves it unchanged,
-  // so summing every slot equals skipping those -- without reading the ids
-  // again here.
-  if (sl == 0) red[t * 8 + r] = valid ? v : 0.0f;
   __syncthreads();
-  if (threadIdx.x < 8) {
+  if (threadIdx.x < 8 * R) {
     float sum = 0.0f;
-    for (int s = 0; s < topk; ++s) sum += red[s * 8 + threadIdx.x];
-    out[(int64_t)m * ld_out + blockIdx.x * 8 + threadIdx.x] = (uint16_t)f32_to_bf16(sum);
+    for (int s = 0; s < topk; ++s) sum += red[s * 8 * R + threadIdx.x];
+    out[(int64_t)m * ld_out + rb0 + threadIdx.x] = (uint16_t)f32_to_bf16(sum);
   }
+}
+
+// Output rows per workgroup of the one-launch w2 + top-k sum, in blocks of 8
+// (each lane owns R rows): R = 2 from 3 tokens up, else 1.  Measured on
+// MI355X (E=256, top-10, K=3072, N=1024): M=4 18.2 -> 16.9 us for the w2
+// launch with R = 2; M=1 7.2 -> 7.6 us and M=2 11.3 -> 11.7 us, so those
+// keep R = 1; R = 4 is slower at every M.
+constexpr int kW2TokenRMax = 2;
+constexpr int kW2TokenR2MinM = 3;
+int pick_w2_token_r(int M, int K) {
+  return (M >= kW2TokenR2MinM && K % (8 * kW2TokenRMax) == 0) ? kW2TokenRMax : 1;
 }
 
 size_t w2_token_lds_bytes(int topk, int kdim) {
   return (size_t)topk * (staged_row_octets(kdim) * sizeof(u32x4_t) +
                          (size_t)((kdim >> 5) + 1) * sizeof(float)) +
-         (size_t)topk * 8 * sizeof(float);
+         (size_t)topk * 8 * kW2TokenRMax * sizeof(float);
 }
 
 
@@ -265,13 +284,18 @@ hipError_t launch_w2_token(const GemvLaunch& a_in, uint16_t* out, int64_t ld_out
   a.nib_magic = 0x43004300u;
   if (!w2_token_fits(a.topk, a.n_out, a.kdim)) return hipErrorInvalidValue;
   const int M = a.n_tok / a.topk;
-  const dim3 grid((unsigned)(a.n_out / 8), (unsigned)M), block(64 * a.topk);
+  const int R = pick_w2_token_r(M, a.n_out);
+  const dim3 grid((unsigned)(a.n_out / (8 * R)), (unsigned)M), block(64 * a.topk);
   const size_t lds = w2_token_lds_bytes(a.topk, a.kdim);
   const int n_it = ((a.kdim >> 5) + 7) >> 3;
-  if (n_it == 4)
-    hipLaunchKernelGGL(w2_token_kernel<4>, grid, block, lds, stream, a, out, ld_out);
+  if (n_it == 4 && R == 2)
+    hipLaunchKernelGGL((w2_token_kernel<4, 2>), grid, block, lds, stream, a, out, ld_out);
+  else if (n_it == 4)
+    hipLaunchKernelGGL((w2_token_kernel<4, 1>), grid, block, lds, stream, a, out, ld_out);
+  else if (R == 2)
+    hipLaunchKernelGGL((w2_token_kernel<0, 2>), grid, block, lds, stream, a, out, ld_out);
   else
-    hipLaunchKernelGGL(w2_token_kernel<0>, grid, block, lds, stream, a, out, ld_out);
+    hipLaunchKernelGGL((w2_token_kernel<0, 1>), grid, block, lds, stream, a, out, ld_out);
   return hipGetLastError();
 }
 
