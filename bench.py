@@ -74,7 +74,10 @@ CALIB_BYTES = 2**30            # plain device copy: PMC byte-counter scale and m
 # Kernel-name fragments of the dominant kernels in rocprofv3 counter files,
 # per stage and path (dequant-GEMV for few pairs per expert, MFMA tiles else).
 KERNEL_KEYS = {("w13", "gemv"): "gemv_kernel<0,", ("w2", "gemv"): "gemv_kernel<1,",
-               ("w13", "mfma"): "mfma_kernel<0,", ("w2", "mfma"): "mfma_kernel<1,"}
+               ("w13", "mfma"): "mfma_kernel<0,", ("w2", "mfma"): "mfma_kernel<1,",
+               ("w13", "mixed"): "mixed_kernel<0,", ("w2", "mixed"): "mixed_kernel<1,"}
+KERNEL_LABELS = {"gemv": "dequant-GEMV (gemv_kernel)", "mfma": "dequant-MFMA tiles (mfma_kernel)",
+                 "mixed": "GEMV and MFMA work items in one launch (mixed_kernel)"}
 
 
 def log(*a):
@@ -570,11 +573,14 @@ def stage_roofline(wl, stage, us):
     nbytes = sum(getattr(wl, f"{stage}_bytes")) / len(wl.sets)
     rows_k = 2 * shape.N * shape.K if stage == "w13" else shape.K * shape.N
     flops = 2 * M * shape.topk * rows_k
-    path = "mfma" if mfma_pair_share(wl) >= 0.5 else "gemv"
+    share = mfma_pair_share(wl)
+    if 0.0 < share < 1.0 and wl.stage_launches()[STAGES.index(stage)] == 1:
+        path = "mixed"  # the split dispatch's two kinds of work items, one launch
+    else:
+        path = "mfma" if share >= 0.5 else "gemv"
     sec = us * 1e-6
     hbm_bound = nbytes / (HBM_PEAK_GBS * 1e9) >= flops / (BF16_PEAK_TFLOPS * 1e12)
-    kernel = (f"{stage} dequant-GEMV (gemv_kernel)" if path == "gemv"
-              else f"{stage} dequant-MFMA tiles (mfma_kernel)")
+    kernel = f"{stage} {KERNEL_LABELS[path]}"
     if hbm_bound:
         achieved, peak, unit = nbytes / sec / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
