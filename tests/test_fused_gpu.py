@@ -484,27 +484,29 @@ def test_mfma_tile_heights_bit_identical(pkg, orc, synth, dev, E, topk, K, N, M,
                f"tile 64 E={E} K={K} N={N} G={group} M={M}", bf16_experts=set(range(E)))
 
 
-@pytest.mark.parametrize("M,skewed,max_tokens,tc", [(64, True, 4, 0), (48, False, 4, 0),
-                                                     (32, True, 2, 2), (256, False, 2, 2)])
-def test_mixed_launch_bit_identical(pkg, orc, synth, dev, M, skewed, max_tokens, tc):
+@pytest.mark.parametrize("M,skewed,max_tokens,tc,E,group",
+                         [(64, True, 4, 0, 256, 32), (48, False, 4, 0, 256, 32),
+                          (32, True, 2, 2, 256, 32), (256, False, 2, 2, 256, 32),
+                          (48, False, 4, 0, 64, 64), (40, True, 4, 2, 64, 128)])
+def test_mixed_launch_bit_identical(pkg, orc, synth, dev, M, skewed, max_tokens, tc, E, group):
     """The split dispatch with 64-slot tiles runs each GEMM's GEMV and MFMA
     work items in one mixed launch; 128-slot tiles (the 8-wave MFMA
     geometry, no mixed kernel) keep two launches per GEMM.  Every work item
     computes what its own launch computes and the tile height does not
     change any sum, so both give the same bits; the mixed result matches
     the oracle."""
-    shape = synth.LayerShape(E=256, topk=10, K=3072, N=1024, group=32)
+    shape = synth.LayerShape(E=E, topk=10, K=3072, N=1024, group=group)
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=29, skewed=skewed)
     L = pkg._lib
     outs = []
     for tm, launches in ((64, [1, 1, 1, 1]), (128, [1, 2, 2, 1])):
         t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=max_tokens, mfma_tile_m=tm,
                        gemv_tokens_per_pass=tc)
-        assert L.stage_launches(M, 10, 256, 1024, 3072, 32, t.to_struct()) == launches
-        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=t))
+        assert L.stage_launches(M, 10, E, 1024, 3072, group, t.to_struct()) == launches
+        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, group, tuning=t))
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
-    hot = mfma_experts(pkg, ti, 256, 1024, 3072, pkg.Tuning(gemv_max_tokens=max_tokens))
+    hot = mfma_experts(pkg, ti, E, 1024, 3072, pkg.Tuning(gemv_max_tokens=max_tokens))
     assert 0 < len(hot) < len(set(ti.reshape(-1).tolist()))  # both kinds of work items
-    _check(orc, outs[0], x, w13, w2, s13, s2, tw, ti, 32, f"mixed M={M} skewed={skewed}",
-           bf16_experts=hot)
+    _check(orc, outs[0], x, w13, w2, s13, s2, tw, ti, group,
+           f"mixed M={M} skewed={skewed} E={E} G={group}", bf16_experts=hot)
