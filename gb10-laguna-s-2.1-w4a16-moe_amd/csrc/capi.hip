@@ -268,13 +268,16 @@ struct FusedArgs {
   const w4a16_moe_tuning* tuning;  // null: built-in choices
 };
 
-// The MFMA kernels address activation rows with 32-bit byte offsets from the
-// row base: the last hidden row (w13) and the last intermediate row (w2) must
-// start below this.
+// The MFMA kernels address activation and output rows with 32-bit byte
+// offsets from the buffer base: the hidden rows (w13 input), the
+// intermediate rows (w13 output, w2 input) and the partial rows (w2 output)
+// must each lie below this.
 constexpr int64_t kMfmaActBytesMax = (int64_t)UINT32_MAX - 4096;
 
-bool mfma_act_fits(int64_t M, int64_t topk, int64_t N, int64_t ld_hidden) {
-  return M * ld_hidden * 2 <= kMfmaActBytesMax && M * topk * N * 2 <= kMfmaActBytesMax;
+bool mfma_act_fits(int64_t M, int64_t topk, int64_t N, int64_t K, int64_t ld_hidden) {
+  const int64_t partial_elt = M > kFp32PartialMaxM ? 2 : 4;
+  return M * ld_hidden * 2 <= kMfmaActBytesMax && M * topk * N * 2 <= kMfmaActBytesMax &&
+         M * topk * K * partial_elt <= kMfmaActBytesMax;
 }
 
 int validate(const FusedArgs& a, Layout* L) {
@@ -289,7 +292,8 @@ int validate(const FusedArgs& a, Layout* L) {
       !a.out || !a.ws)
     return W4A16_ERR_NULL_POINTER;
   if (a.ld_hidden < a.K || a.ld_out < a.K) return W4A16_ERR_INVALID_SHAPE;
-  if (L->mfma && !mfma_act_fits(a.M, a.topk, a.N, a.ld_hidden)) return W4A16_ERR_INVALID_SHAPE;
+  if (L->mfma && !mfma_act_fits(a.M, a.topk, a.N, a.K, a.ld_hidden))
+    return W4A16_ERR_INVALID_SHAPE;
   if (a.ws_bytes < L->total) return W4A16_ERR_WORKSPACE_TOO_SMALL;
   if (!aligned(a.hidden, 16) || a.ld_hidden % 8 != 0) return W4A16_ERR_MISALIGNED;
   if (!aligned(a.w13, 16) || !aligned(a.w2, 16)) return W4A16_ERR_MISALIGNED;

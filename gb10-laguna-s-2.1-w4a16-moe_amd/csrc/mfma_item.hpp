@@ -76,6 +76,10 @@ constexpr int kUnroll = 4;                   // double steps per loop iteration
 #define W4A16_MFMA_KSPLIT -1
 #endif
 constexpr int kMfmaSplit = W4A16_MFMA_KSPLIT;
+// Raw buffer resource word 3 (gfx9: no format, no swizzle) and a byte offset
+// past any buffer's end (the store is dropped).
+constexpr int kRawBufferWord3 = 0x00020000;
+constexpr uint32_t kDropOffset = 0xFFFFFFF0u;
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
@@ -330,6 +334,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   constexpr int kWslotsG = G::kWslots;
   constexpr int DW = G::kDW;
   static_assert(steady_wait_safe(NA, DW, GSHIFT == 1 ? 2 : 1), "DMA wait counts");
+  static_assert(dmas_behind(17, NA, DW, GSHIFT == 1 ? 2 : 1) + MC * 2 < 64, "vmcnt range");
   static_assert(dmas_behind(19, NA, DW, GSHIFT == 1 ? 2 : 1) < 64, "vmcnt range");
   // Slot of weight pair p, from the slot of pair 2 it (wave-uniform).
   auto wslot = [](int base, int c) {
@@ -500,38 +505,103 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // Output of row tile nt.  Accumulator register r of a 32x32 block holds
   // weight row 8 (r / 4) + 4 q + r % 4 of the wave's block and token slot j;
   // the slot's token row and routing weight (w2) are in LDS (s_f, s_wt).
+  // The epilogue's stores: raw buffer stores over the output rows, issued by
+  // every lane -- a slot past the tile's pairs stores at an offset past the
+  // buffer's end, which the hardware drops -- so a row tile's epilogue issues
+  // the same number of vector-memory instructions on every wave, at least
+  // kEpiStores.  Lanes q = 0 and q = 1 of slot j hold alternating runs of 4
+  // outputs; v_permlane32_swap trades runs between the two halves of the
+  // wave so that each lane stores 8 consecutive outputs (16 bytes) at once,
+  // and for w2 v_permlane16_swap then trades pieces between slots j and
+  // j + 16 so that each store instruction writes 16 slots x 64 bytes (the
+  // wave's 32 rows of each) instead of 32 slots x 32 bytes: a quarter of the
+  // store instructions and write requests of storing each run of 4 on its
+  // own.
+  constexpr int kEpiStores = MC * (MODE == 0 ? 1 : 2);
+  const uint32_t out_elt = (MODE == 1 && !a.partial_bf16) ? 4u : 2u;
+  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      a.out, 0, (uint32_t)a.n_tok * (uint32_t)a.n_out * out_elt, kRawBufferWord3);
+  // swap_halves(a, b): the a of lanes 32-63 and the b of lanes 0-31 trade
+  // places -- lanes 0-31 keep their a and get, as b, the a of lane + 32;
+  // lanes 32-63 get, as a, the b of lane - 32 and keep their b.
+  auto swap_halves = [](u32x2_t& a2, u32x2_t& b2) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const auto r = __builtin_amdgcn_permlane32_swap(a2[w], b2[w], false, false);
+      a2[w] = r[0];
+      b2[w] = r[1];
+    }
+  };
+  // swap_rows16(a, b): the a of lane rows 1 and 3 (lanes 16-31, 48-63) and
+  // the b of rows 0 and 2 trade places -- lanes of rows 0, 2 keep their a
+  // and get, as b, the a of lane + 16; lanes of rows 1, 3 get, as a, the b
+  // of lane - 16 and keep their b.
+  auto swap_rows16 = [](u32x2_t& a2, u32x2_t& b2) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const auto r = __builtin_amdgcn_permlane16_swap(a2[w], b2[w], false, false);
+      a2[w] = r[0];
+      b2[w] = r[1];
+    }
+  };
+  auto store16 = [&](const u32x2_t& lo, const u32x2_t& hi, uint32_t byte_off) {
+    const u32x4_t v = {lo[0], lo[1], hi[0], hi[1]};
+    __builtin_amdgcn_raw_buffer_store_b128(v, out_rsrc, byte_off, 0, 0);
+  };
   auto write_out = [&](int nt) {
 #pragma unroll
     for (int m = 0; m < MC; ++m) {
       const int f = s_f[32 * m + j];
-      if (f >= a.n_tok) continue;
+      const bool live = f < a.n_tok;  // the same for both lanes of a slot
       if (MODE == 0) {
-        // r < 8: gate column 8 (r / 4) + 4 q + r % 4 of the wave's 16; r + 8:
-        // its up row.
-        uint16_t* out = static_cast<uint16_t*>(a.out) + (int64_t)f * a.n_out +
-                        nt * (kTileN / 2) + 16 * wid + 4 * q;
+        // Lane (q, j): r < 8 gate column 8 (r / 4) + 4 q + r % 4 of the
+        // wave's 16, r + 8 its up row; runs i4 = 0, 1 are columns 4 q + 0..3
+        // and 8 + 4 q + 0..3.  After the swap lane q holds columns 8 q .. +7.
+        u32x2_t hv[2];
 #pragma unroll
         for (int i4 = 0; i4 < 2; ++i4) {
           float h[4];
 #pragma unroll
           for (int c = 0; c < 4; ++c) h[c] = silu(acc[m][4 * i4 + c]) * acc[m][8 + 4 * i4 + c];
-          *reinterpret_cast<u32x2_t*>(out + 8 * i4) =
-              u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+          hv[i4] = u32x2_t{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
         }
+        swap_halves(hv[0], hv[1]);
+        const uint32_t e0 =
+            (uint32_t)f * (uint32_t)a.n_out + nt * (kTileN / 2) + 16 * wid + 8 * q;
+        store16(hv[0], hv[1], live ? e0 * 2u : kDropOffset);
       } else {
+        // Lane (q, j): runs i4 = 0..3 are rows 8 i4 + 4 q + 0..3 of the
+        // wave's 32 for slot j.  After the half swaps lane (q, j) holds rows
+        // 8 q .. +7 (runs 0, 1) and 16 + 8 q .. +7 (runs 2, 3); after the row
+        // swaps its first piece is rows 16 h + 8 q .. +7 of slot j % 16 and
+        // its second the same rows of slot 16 + j % 16 (h = j / 16).
         const float wt = s_wt[32 * m + j];
-        const int64_t base = (int64_t)f * a.n_out + nt * kTileN + 32 * wid + 4 * q;
+        const uint32_t e0 = (uint32_t)f * (uint32_t)a.n_out + nt * kTileN + 32 * wid;
+        if (a.partial_bf16) {
+          u32x2_t pv[4];
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int64_t o = base + 8 * i4;
-          const float v0 = acc[m][4 * i4 + 0] * wt, v1 = acc[m][4 * i4 + 1] * wt;
-          const float v2 = acc[m][4 * i4 + 2] * wt, v3 = acc[m][4 * i4 + 3] * wt;
-          if (a.partial_bf16) {
-            *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(a.out) + o) =
-                u32x2_t{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-          } else {
-            *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.out) + o) =
-                f32x4_t{v0, v1, v2, v3};
+          for (int i4 = 0; i4 < 4; ++i4)
+            pv[i4] = u32x2_t{pack_bf16x2(acc[m][4 * i4 + 0] * wt, acc[m][4 * i4 + 1] * wt),
+                             pack_bf16x2(acc[m][4 * i4 + 2] * wt, acc[m][4 * i4 + 3] * wt)};
+          swap_halves(pv[0], pv[1]);
+          swap_halves(pv[2], pv[3]);
+          swap_rows16(pv[0], pv[2]);
+          swap_rows16(pv[1], pv[3]);
+          const int f1 = s_f[32 * m + (j & 15)], f2 = s_f[32 * m + (j | 16)];
+          const uint32_t rows = nt * kTileN + 32 * wid + 16 * (j >> 4) + 8 * q;
+          store16(pv[0], pv[1],
+                  f1 < a.n_tok ? ((uint32_t)f1 * (uint32_t)a.n_out + rows) * 2u : kDropOffset);
+          store16(pv[2], pv[3],
+                  f2 < a.n_tok ? ((uint32_t)f2 * (uint32_t)a.n_out + rows) * 2u : kDropOffset);
+        } else {
+          // fp32 partials (few-token calls): 4 rows are already 16 bytes.
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const f32x4_t v = {acc[m][4 * i4 + 0] * wt, acc[m][4 * i4 + 1] * wt,
+                               acc[m][4 * i4 + 2] * wt, acc[m][4 * i4 + 3] * wt};
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4_t, v), out_rsrc,
+                live ? (e0 + 8 * i4 + 4 * q) * 4u : kDropOffset, 0, 0);
           }
         }
       }
@@ -569,6 +639,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   const int n_it = nrt * IT;
   int rt_cur = 0;
   int ws0 = 0;  // slot of weight pair 2 it
+  bool post_epi = false;  // this iteration follows a row tile's epilogue
   for (int it = 0; it < n_it; ++it) {
     // One double step; tp = t % 4 is a compile-time constant.
     auto step = [&](auto tp_c) {
@@ -632,7 +703,18 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       // Step t+1's data (activations, weight pair, scales) has landed once
       // at most dmas_behind(t) of this wave's DMAs are in flight; the count
       // depends on t % 4 only.
-      wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
+      // In the iteration after a row tile's epilogue, steps 0 and 1 wait for
+      // data whose DMAs were issued before the epilogue's stores: those
+      // stores are still allowed in flight.  (From step 2 on the awaited
+      // DMAs were issued after the stores, which therefore land first.)
+      if constexpr (tp < 2) {
+        if (post_epi)
+          wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas) + kEpiStores>();
+        else
+          wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
+      } else {
+        wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
+      }
       read_w_operands(tn, wslot(ws0, (tp + 1) / 2), tp == 3 ? ((it + 1) & 1) : (it & 1));
       __builtin_amdgcn_sched_barrier(0);
       constexpr int kSplit = kMfmaSplit < 0 ? (MC + 1) / 2 : (kMfmaSplit > MC ? MC : kMfmaSplit);
@@ -654,18 +736,22 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
     step(std::integral_constant<int, 1>{});
     step(std::integral_constant<int, 2>{});
     step(std::integral_constant<int, 3>{});
+    post_epi = false;
     if (it + 1 == (rt_cur + 1) * IT) {
       write_out(nt0 + rt_cur);
       clear_acc();
       ++rt_cur;
+      post_epi = true;
     }
     ws0 = wslot(ws0, 2);
   }
   // The reads of a step past the last (clamped DMAs, never used) are the
   // only LDS reads still in flight.
   wait_lgkmcnt0();
-  // No LDS DMA may still be in flight when the workgroup's LDS is released.
-  wait_vmcnt<0>();
+  // No LDS DMA may still be in flight when the workgroup's LDS is released:
+  // every DMA was issued before the last epilogue's stores, which need not
+  // land before the workgroup ends.
+  wait_vmcnt<kEpiStores>();
 }
 
 // One work item of a launch: `bid` is the workgroup's index in the launch's
@@ -742,9 +828,11 @@ bool mfma_fits(const MfmaLaunch& a) {
   if (rows_total % G::kTN != 0 || a.kdim % (kStepK * kUnroll) != 0) return false;
   if (a.tile_m < 32 || a.tile_m > G::kTM) return false;
   if (reinterpret_cast<uintptr_t>(a.s) % 16 != 0) return false;
-  // Activation rows are addressed with 32-bit byte offsets.
+  // Activation rows and output rows are addressed with 32-bit byte offsets.
   const int64_t act_rows = MODE == 0 ? a.n_tok / a.topk : a.n_tok;
   if (act_rows * a.ld_act * 2 > (int64_t)UINT32_MAX - 4096) return false;
+  const int64_t out_elt = (MODE == 1 && !a.partial_bf16) ? 4 : 2;
+  if ((int64_t)a.n_tok * a.n_out * out_elt > (int64_t)UINT32_MAX - 4096) return false;
   if (a.row_tiles < 1) return false;
   // The DMAs run up to kDW double steps ahead, within the next two row tiles.
   return 2 * (a.kdim / kStepK) > G::kDW;

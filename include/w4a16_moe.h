@@ -147,10 +147,11 @@ int w4a16_moe_workspace_layout(int64_t M, int64_t topk, int64_t num_experts,
  * M * topk < 2^30; hidden and packed-weight pointers 16-byte aligned;
  * ld_hidden % 8 == 0; workspace 256-byte aligned and at least
  * w4a16_moe_workspace_size bytes.  Calls that run the MFMA kernels (M above
- * the GEMV-only bound, N and K multiples of 256) address activation rows
- * with 32-bit byte offsets: they also need M * ld_hidden * 2 and
- * M * topk * N * 2 at most 2^32 - 4097 bytes (W4A16_ERR_INVALID_SHAPE
- * otherwise, before any GPU work).
+ * the GEMV-only bound, N and K multiples of 256) address activation and
+ * output rows with 32-bit byte offsets: they also need M * ld_hidden * 2,
+ * M * topk * N * 2 and M * topk * K * 2 (* 4 when M <= 4) at most
+ * 2^32 - 4097 bytes (W4A16_ERR_INVALID_SHAPE otherwise, before any GPU
+ * work); at K = 3072, topk = 10 that is M <= 69,904.
  */
 int w4a16_moe_fused_experts(const void* hidden, int64_t ld_hidden,
                             const void* w13_packed, const void* w2_packed,

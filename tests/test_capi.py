@@ -184,6 +184,11 @@ def test_mfma_activation_offset_limit_is_a_shape_error(lib, pkg):
     # offsets: the same stride passes the shape checks (and stops at the
     # workspace check, still before any GPU work)
     assert _fused(lib, M=16, ld_hidden=ld, ws_bytes=0) == L.W4A16_ERR_WORKSPACE_TOO_SMALL
+    # the w2 partial rows (M * topk * K * 2 bytes) are an output of the MFMA
+    # kernels, addressed the same way: 69,904 tokens fit, 69,905 do not
+    for M, want in ((69904, L.W4A16_ERR_WORKSPACE_TOO_SMALL),
+                    (69905, L.W4A16_ERR_INVALID_SHAPE)):
+        assert _fused(lib, M=M, ld_hidden=3072, ws_bytes=0) == want
 
 
 @pytest.mark.parametrize("M,want", [(0, [0, 0, 0, 0]), (1, [0, 1, 1, 0]), (4, [0, 1, 1, 0]),
