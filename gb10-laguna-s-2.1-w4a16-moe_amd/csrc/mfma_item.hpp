@@ -509,7 +509,8 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // every lane -- a slot past the tile's pairs stores at an offset past the
   // buffer's end, which the hardware drops -- so a row tile's epilogue issues
   // the same number of vector-memory instructions on every wave, at least
-  // kEpiStores.  Lanes q = 0 and q = 1 of slot j hold alternating runs of 4
+  // kEpiStores, and the workgroup's last wait leaves them in flight.  Lanes
+  // q = 0 and q = 1 of slot j hold alternating runs of 4
   // outputs; v_permlane32_swap trades runs between the two halves of the
   // wave so that each lane stores 8 consecutive outputs (16 bytes) at once,
   // and for w2 v_permlane16_swap then trades pieces between slots j and
@@ -639,7 +640,6 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   const int n_it = nrt * IT;
   int rt_cur = 0;
   int ws0 = 0;  // slot of weight pair 2 it
-  bool post_epi = false;  // this iteration follows a row tile's epilogue
   for (int it = 0; it < n_it; ++it) {
     // One double step; tp = t % 4 is a compile-time constant.
     auto step = [&](auto tp_c) {
@@ -703,18 +703,10 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
       // Step t+1's data (activations, weight pair, scales) has landed once
       // at most dmas_behind(t) of this wave's DMAs are in flight; the count
       // depends on t % 4 only.
-      // In the iteration after a row tile's epilogue, steps 0 and 1 wait for
-      // data whose DMAs were issued before the epilogue's stores: those
-      // stores are still allowed in flight.  (From step 2 on the awaited
-      // DMAs were issued after the stores, which therefore land first.)
-      if constexpr (tp < 2) {
-        if (post_epi)
-          wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas) + kEpiStores>();
-        else
-          wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
-      } else {
-        wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
-      }
+      // (After a row tile's epilogue the first waits also wait for its
+      // stores: counting them instead, measured, gained nothing on w2 and
+      // cost w13 ~2 % through the loop's code.)
+      wait_vmcnt<dmas_behind(4 * kUnroll + tp, NA, DW, kSDmas)>();
       read_w_operands(tn, wslot(ws0, (tp + 1) / 2), tp == 3 ? ((it + 1) & 1) : (it & 1));
       __builtin_amdgcn_sched_barrier(0);
       constexpr int kSplit = kMfmaSplit < 0 ? (MC + 1) / 2 : (kMfmaSplit > MC ? MC : kMfmaSplit);
@@ -736,12 +728,10 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
     step(std::integral_constant<int, 1>{});
     step(std::integral_constant<int, 2>{});
     step(std::integral_constant<int, 3>{});
-    post_epi = false;
     if (it + 1 == (rt_cur + 1) * IT) {
       write_out(nt0 + rt_cur);
       clear_acc();
       ++rt_cur;
-      post_epi = true;
     }
     ws0 = wslot(ws0, 2);
   }
