@@ -77,7 +77,7 @@ constexpr int kUnroll = 4;                   // double steps per loop iteration
 #endif
 constexpr int kMfmaSplit = W4A16_MFMA_KSPLIT;
 // Raw buffer resource word 3 (gfx9: no format, no swizzle) and a byte offset
-// past any buffer's end (the store is dropped).
+// past any buffer's end (a store there is dropped, a load returns zeros).
 constexpr int kRawBufferWord3 = 0x00020000;
 constexpr uint32_t kDropOffset = 0xFFFFFFF0u;
 
@@ -180,6 +180,15 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint3
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(voff), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+// The same 16-byte LDS DMA from a raw buffer: a lane whose offset is past the
+// buffer's end writes zeros.
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
+                                              uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 __device__ __forceinline__ void lds_dma4(const void* base, uint32_t voff, uint32_t lds) {
@@ -348,7 +357,9 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // of them (the caller instantiates both counts of an uneven share); DMA k
   // fills rows 8 k .. 8 k + 7 of the buffer: lane l writes row r = 8 k + l / 8
   // at chunk position l % 8, so it fetches chunk (l % 8) ^ g(r) of that row.
-  // Rows of padding slots read row 0.
+  // Lanes of padding slots read past the end of the activation buffer, so
+  // their rows are zeros: the MFMAs over them compute what they would with
+  // any row (their outputs are not stored) and draw less power.
   static_assert(NA >= 0 && NA <= (4 * MC + kWaves - 1) / kWaves, "activation DMAs per wave");
   constexpr int kNA1 = NA > 0 ? NA : 1;
   uint32_t a_off[kNA1];  // byte offset of this lane's source row + chunk
@@ -359,16 +370,23 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
     a_dst[i] = k * 1024;
     const int r = 8 * k + (lane >> 3);
     const int f = s_f[r];
-    uint32_t row = 0;
-    if (f < a.n_tok) row = MODE == 0 ? (uint32_t)(f / a.topk) : (uint32_t)f;
+    const uint32_t row = MODE == 0 ? (uint32_t)(f / a.topk) : (uint32_t)f;
     const int g = (lane >> 3) ^ (k & 7);  // swizzle of row r (see above)
-    a_off[i] = row * (uint32_t)a.ld_act * 2u + (uint32_t)(((lane & 7) ^ g) * 16);
+    a_off[i] = f < a.n_tok ? row * (uint32_t)a.ld_act * 2u + (uint32_t)(((lane & 7) ^ g) * 16)
+                           : kDropOffset;
   }
   const char* const act = reinterpret_cast<const char*>(a.act);
-  // The item's row tiles share the activation rows: local step k of any.
+  const uint32_t act_bytes = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(MODE == 0 ? a.n_tok / a.topk : a.n_tok) * (uint32_t)a.ld_act * 2u);
+  // The item's row tiles share the activation rows: local step k of any.  The
+  // step's column offset moves the buffer's base, so that the padding lanes'
+  // offset stays past the end; a live lane's bytes end within row f, before
+  // act_bytes.
   auto dma_a1 = [&](int k, int buf, int i) {
-    const uint32_t koff = (uint32_t)k * (kStepK * 2);
-    lds_dma16(act, a_off[i] + koff, lds_addr(lds + buf * kAbufG + a_dst[i]));
+    const uint32_t koff = __builtin_amdgcn_readfirstlane((uint32_t)k * (kStepK * 2));
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(act + koff), 0, act_bytes, kRawBufferWord3);
+    lds_dma16_buf(rsrc, a_off[i], lds_addr(lds + buf * kAbufG + a_dst[i]));
   };
   auto dma_a = [&](int k, int buf) {
 #pragma unroll
