@@ -45,7 +45,7 @@ struct Tuning {
   int lpr;              // GEMV lanes per weight row (0 = launcher's choice)
   int w2_fused_max_m;   // M at or below this: w2 and the top-k sum as one kernel
   bool auto_split;      // gemv_max_tokens is the built-in choice (see compute_layout)
-  int row_tiles;        // MFMA row tiles per work item (0 = built-in per GEMM)
+  int row_tiles;        // 256-row weight blocks per MFMA work item (0 = built-in per GEMM)
 };
 
 struct Layout {
@@ -67,7 +67,7 @@ struct Layout {
   int tc;
   int upw;
   int lpr;
-  int row_tiles_w13;  // MFMA row tiles per work item
+  int row_tiles_w13;  // 256-row weight blocks per MFMA work item
   int row_tiles_w2;
 };
 
@@ -103,9 +103,19 @@ constexpr bool kMixedLaunches = W4A16_MIXED_LAUNCHES != 0;
 // K=3072, N=1024), best per GEMM: M=4096 w13 1 (578 us vs 597 at 2), w2 2
 // (371 vs 394 at 1); M=1024 w13 4 (283 vs 331 at 1), w2 6 (161 vs 211 at
 // 1); skewed M=64 w13 1 (99 vs 118 at 4).  Every choice is bit-identical.
+// These are the 192- and 128-slot tiles; the 64-slot tiles use
+// kSmallItemRows* below.
 constexpr double kItemWorkW13 = 330.0;
 constexpr double kItemWorkW2 = 180.0;
 constexpr int64_t kCUs = 256;  // MI355X
+// Built-in weight rows per work item of the 64-slot tiles (4-wave
+// workgroups, 128-row row tiles).  Measured on MI355X (E=256, top-10,
+// K=3072, N=1024) over M=32-512, uniform and skewed routing, 128, 256 or 512
+// rows per item: w2 is fastest at 512 everywhere (5-10 % below 128: skewed
+// M=64 40.7 vs 44.8 us, uniform M=192 113 vs 123 us), w13 at 256 or within
+// 1 % of it (uniform M=256 228 vs 237 us against 128).
+constexpr int64_t kSmallItemRowsW13 = 256;
+constexpr int64_t kSmallItemRowsW2 = 512;
 
 int pick_row_tiles(int64_t n_tiles_n, int64_t steps, int64_t n_tok, int64_t E,
                    double item_work) {
@@ -122,6 +132,14 @@ int pick_row_tiles(int64_t n_tiles_n, int64_t steps, int64_t n_tok, int64_t E,
     const double d = std::fabs(std::log((double)r / want));
     if (d < best_d) best_d = d, best = r;
   }
+  return best;
+}
+// The largest divisor of n_blocks (256-row weight blocks of a GEMM) of at
+// most `rows` weight rows.
+int small_row_tiles(int64_t n_blocks, int64_t rows) {
+  int best = 1;
+  for (int r = 1; r <= n_blocks && r * (int64_t)kMfmaTileN <= rows; ++r)
+    if (n_blocks % r == 0) best = r;
   return best;
 }
 // Average (token, slot) pairs per expert from which the built-in split sends
@@ -202,10 +220,6 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
   // every expert goes to the MFMA kernels and the GEMV launches are skipped.
   if (L->mfma && T.auto_split && (int64_t)n_tok >= kAllMfmaMinPairs * E) L->gemv_max_tokens = 0;
   L->gemv = !L->mfma || L->gemv_max_tokens > 0;
-  L->row_tiles_w13 = T.row_tiles > 0 ? T.row_tiles
-                                      : pick_row_tiles(2 * N / kMfmaTileN, K / 64, n_tok, E, kItemWorkW13);
-  L->row_tiles_w2 = T.row_tiles > 0 ? T.row_tiles
-                                     : pick_row_tiles(K / kMfmaTileN, N / 64, n_tok, E, kItemWorkW2);
   L->tc = T.tc;
   L->upw = T.upw;
   L->lpr = T.lpr;
@@ -217,6 +231,15 @@ int compute_layout(int64_t M, int64_t topk, int64_t E, int64_t N, int64_t K,
                        : ((int64_t)n_tok < kTile64MaxPairs * E    ? kMfmaTileMSmall
                           : (int64_t)n_tok < kTile128MaxPairs * E ? kMfmaTileMMin
                                                                   : kMfmaTileMMax);
+  if (T.row_tiles > 0) {
+    L->row_tiles_w13 = L->row_tiles_w2 = T.row_tiles;
+  } else if (L->tile_m <= kMfmaTileMSmall) {
+    L->row_tiles_w13 = small_row_tiles(2 * N / kMfmaTileN, kSmallItemRowsW13);
+    L->row_tiles_w2 = small_row_tiles(K / kMfmaTileN, kSmallItemRowsW2);
+  } else {
+    L->row_tiles_w13 = pick_row_tiles(2 * N / kMfmaTileN, K / 64, n_tok, E, kItemWorkW13);
+    L->row_tiles_w2 = pick_row_tiles(K / kMfmaTileN, N / 64, n_tok, E, kItemWorkW2);
+  }
   L->max_tiles = L->mfma ? (int64_t)n_tok / L->tile_m + heavy : 0;
   L->max_gemv = L->mfma ? std::min<int64_t>(std::min<int64_t>(E, (int64_t)n_tok), L->nb)
                         : std::min<int64_t>((int64_t)n_tok, L->nb);
@@ -387,6 +410,8 @@ MfmaLaunch mfma_args(const FusedArgs& a, const Layout& L, const Work& w, int mod
   m.group = (int32_t)a.group;
   m.max_tiles = (int32_t)L.max_tiles;
   m.tile_m = L.tile_m;
+  // The kernels count row tiles of their geometry's height.
+  const int row_scale = L.tile_m <= kMfmaTileMSmall ? kMfmaTileN / kMfmaTileNSmall : 1;
   if (mode == 0) {
     m.act = static_cast<const uint16_t*>(a.hidden);
     m.ld_act = a.ld_hidden;
@@ -396,7 +421,7 @@ MfmaLaunch mfma_args(const FusedArgs& a, const Layout& L, const Work& w, int mod
     m.out = w.inter;
     m.n_out = (int32_t)a.N;
     m.kdim = (int32_t)a.K;
-    m.row_tiles = L.row_tiles_w13;
+    m.row_tiles = L.row_tiles_w13 * row_scale;
   } else {
     m.act = w.inter;
     m.ld_act = a.N;
@@ -407,7 +432,7 @@ MfmaLaunch mfma_args(const FusedArgs& a, const Layout& L, const Work& w, int mod
     m.partial_bf16 = L.partial_bf16;
     m.n_out = (int32_t)a.K;
     m.kdim = (int32_t)a.N;
-    m.row_tiles = L.row_tiles_w2;
+    m.row_tiles = L.row_tiles_w2 * row_scale;
   }
   return m;
 }

@@ -97,11 +97,14 @@ namespace w4a16 {
 
 // MFMA tile: token slots x weight rows of one workgroup.  An expert's pairs
 // are cut into the fewest tiles of at most tile_m slots (64, 128 or 192,
-// chosen per call), of near-equal size.
+// chosen per call), of near-equal size.  Tiles of at most 64 slots run on
+// 4-wave workgroups of 128-row row tiles, the others on 8-wave workgroups of
+// 256-row row tiles.
 constexpr int kMfmaTileMSmall = 64;
 constexpr int kMfmaTileMMin = 128;
 constexpr int kMfmaTileMMax = 192;
 constexpr int kMfmaTileN = 256;
+constexpr int kMfmaTileNSmall = 128;
 
 struct AlignLaunch {
   const int32_t* ids;
@@ -203,7 +206,7 @@ struct MfmaLaunch {
   int32_t group;
   int32_t max_tiles;
   int32_t tile_m;          // token slots per tile, at most (128 or 192)
-  int32_t row_tiles;       // row tiles (kMfmaTileN rows) one workgroup runs in turn
+  int32_t row_tiles;       // row tiles (of the geometry's height) one workgroup runs in turn
 };
 hipError_t launch_w13_mfma(const MfmaLaunch& a, hipStream_t stream);
 hipError_t launch_w2_mfma(const MfmaLaunch& a, hipStream_t stream);

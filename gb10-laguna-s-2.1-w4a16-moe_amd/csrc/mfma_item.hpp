@@ -289,6 +289,7 @@ constexpr bool steady_wait_safe(int NA, int DW, int KS) {
 }
 static_assert(BigTile::kTN == kTN, "row tile of the big tiles");
 static_assert(SmallTile::kTM == kMfmaTileMSmall, "small tiles are the 64-slot tiles");
+static_assert(SmallTile::kTN == kMfmaTileNSmall, "row tile of the small tiles");
 
 // One tile of MC token blocks (32 slots each).  GSHIFT = log2(group / 32).
 //

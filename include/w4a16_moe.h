@@ -239,9 +239,11 @@ int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count,
  *                         0 (the library's choice: 4) or a token count.
  *   mfma_row_tiles        256-row weight tiles of one token tile that one MFMA
  *                         workgroup runs in turn, its loads streaming on across
- *                         them: 0 (the library's choice per GEMM, by the
- *                         work per tile) or 1..16 for both (results are
- *                         bit-identical for every value).
+ *                         them: 0 (the library's choice per GEMM: by the
+ *                         work per tile for 128- and 192-slot tiles, 256 rows
+ *                         for w13 and 512 for w2 with 64-slot tiles) or 1..16
+ *                         for both (results are bit-identical for every
+ *                         value).
  * Every choice computes the same function; the
  * GEMV and MFMA kernels differ only in rounding (within the tolerance of
  * fused_experts).  A NULL tuning selects w4a16_moe_default_tuning's values.

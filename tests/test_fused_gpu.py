@@ -445,15 +445,20 @@ def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
     assert mab <= MAX_ABS_MAX
 
 
-@pytest.mark.parametrize("E,topk,K,N,M", [(256, 10, 3072, 1024, 640), (4, 2, 1024, 512, 400)])
-def test_mfma_row_tiles_bit_identical(pkg, synth, dev, E, topk, K, N, M):
+@pytest.mark.parametrize("E,topk,K,N,M,tile_m", [(256, 10, 3072, 1024, 640, 0),
+                                                 (4, 2, 1024, 512, 400, 0),
+                                                 (256, 10, 3072, 1024, 64, 64),
+                                                 (8, 4, 1024, 512, 100, 64)])
+def test_mfma_row_tiles_bit_identical(pkg, synth, dev, E, topk, K, N, M, tile_m):
     """A work item of several row tiles streams its loads on across them but
-    accumulates every row tile exactly as a one-tile item does."""
+    accumulates every row tile exactly as a one-tile item does (64-slot
+    tiles: 128-row row tiles, two per 256-row block of the tuning)."""
     shape = synth.LayerShape(E=E, topk=topk, K=K, N=N, group=32)
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=21)
     outs = []
     for rt in (1, 2, 3, 5, 16):
-        t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=0, mfma_row_tiles=rt)
+        t = pkg.Tuning(gemv_only_max_m=0, gemv_max_tokens=0, mfma_tile_m=tile_m,
+                       mfma_row_tiles=rt)
         outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=t))
     torch.cuda.synchronize()
     for rt, o in zip((2, 3, 5, 16), outs[1:]):
