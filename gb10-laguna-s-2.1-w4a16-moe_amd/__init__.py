@@ -23,11 +23,11 @@ from .routing import router_topk_softmax  # noqa: F401
 from .checkpoint import (  # noqa: F401
     CheckpointError,
     MoELayerWeights,
+    W4A16MoELayer,
     list_moe_layers,
     load_moe_layer,
     save_moe_layer,
 )
-from .layer import W4A16MoELayer  # noqa: F401
 from . import integration  # noqa: F401
 from . import tuning  # noqa: F401
 from .tuning import Tuning  # noqa: F401

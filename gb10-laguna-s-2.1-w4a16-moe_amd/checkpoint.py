@@ -23,6 +23,11 @@ the files:
 No value is changed on the way: the packed words and the scale bits are
 copied as stored.  ``save_moe_layer`` writes the same format (for exports and
 tests).
+
+``W4A16MoELayer`` is one MoE layer over such weights outside vLLM: the two
+launches the reference's serving path makes per layer -- routing (torch.topk
++ softmax, bench/bench_moe.py:225-230) and fused_experts_w4a16
+(kernels/w4a16_moe.py:678-909).
 """
 
 from __future__ import annotations
@@ -35,6 +40,8 @@ from pathlib import Path
 import torch
 
 from . import _lib
+from .routing import router_topk_softmax
+from .w4a16_moe import fused_experts_w4a16
 
 GATE_UP_DOWN = ("gate_proj", "up_proj", "down_proj")  # HF / vLLM default names
 W1_W3_W2 = ("w1", "w3", "w2")                          # Mixtral-style names
@@ -319,3 +326,27 @@ def save_moe_layer(path, prefix: str, w13: torch.Tensor, w2: torch.Tensor,
     p = Path(path)
     save_file(out, str(p))
     return p
+
+
+class W4A16MoELayer:
+    """Router step + fused W4A16 experts over one layer's weights."""
+
+    def __init__(self, weights: MoELayerWeights, topk: int, renormalize: bool = True):
+        self.weights = weights
+        self.topk = int(topk)
+        self.renormalize = bool(renormalize)
+
+    @classmethod
+    def from_checkpoint(cls, source, prefix: str, topk: int, renormalize: bool = True,
+                        device="cuda", names=GATE_UP_DOWN) -> "W4A16MoELayer":
+        return cls(load_moe_layer(source, prefix, device=device, names=names), topk,
+                   renormalize)
+
+    def route(self, router_logits: torch.Tensor):
+        return router_topk_softmax(router_logits, self.topk, self.renormalize)
+
+    def __call__(self, hidden: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
+        w = self.weights
+        topk_weights, topk_ids = self.route(router_logits)
+        return fused_experts_w4a16(hidden, w.w13, w.w2, w.s13, w.s2, topk_weights, topk_ids,
+                                   w.group_size)
