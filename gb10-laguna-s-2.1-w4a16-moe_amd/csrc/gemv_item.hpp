@@ -76,6 +76,25 @@ __device__ __forceinline__ float word_dot(uint32_t w, const u32x4_t& x, float ac
   return acc;
 }
 
+// Octet u of a staged row (below) from its loaded bits d, zero past the
+// row: every lane of the wave calls it (the -C sum crosses a lane quad).
+__device__ __forceinline__ void stage_octet(u32x4_t d, int u, int n_oct, u32x4_t* xp, float* xc,
+                                            int tid) {
+  const float x0 = bf16_to_f32(d[0] & 0xFFFFu), x1 = bf16_to_f32(d[0] >> 16);
+  const float x2 = bf16_to_f32(d[1] & 0xFFFFu), x3 = bf16_to_f32(d[1] >> 16);
+  const float x4 = bf16_to_f32(d[2] & 0xFFFFu), x5 = bf16_to_f32(d[2] >> 16);
+  const float x6 = bf16_to_f32(d[3] & 0xFFFFu), x7 = bf16_to_f32(d[3] >> 16);
+  float c = -136.0f * (((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)));
+  u32x4_t p;
+  p[0] = (d[0] & 0xFFFFu) | (d[2] << 16);      // (x0, x4)
+  p[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);  // (x1, x5)
+  p[2] = (d[1] & 0xFFFFu) | (d[3] << 16);      // (x2, x6)
+  p[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);  // (x3, x7)
+  if (u < n_oct + 4) xp[lds_octet(u)] = p;
+  c = quad_sum(c);  // the 4 octets of a group sit in one lane quad
+  if (u < n_oct + 4 && (tid & 3) == 0) xc[u >> 2] = c;  // -C
+}
+
 // Stage one bf16 activation row of kdim values into LDS, permuted into the
 // pair order word_dot expects, plus the per-group offset correction C.  NT
 // threads take part, thread `tid` (NT a multiple of 64, tid in [0, NT)).
@@ -89,19 +108,7 @@ __device__ __forceinline__ void stage_row(const uint16_t* __restrict__ src, int 
     const int u = u0 + tid;
     u32x4_t d = {0u, 0u, 0u, 0u};
     if (u < n_oct) d = s4[u];
-    const float x0 = bf16_to_f32(d[0] & 0xFFFFu), x1 = bf16_to_f32(d[0] >> 16);
-    const float x2 = bf16_to_f32(d[1] & 0xFFFFu), x3 = bf16_to_f32(d[1] >> 16);
-    const float x4 = bf16_to_f32(d[2] & 0xFFFFu), x5 = bf16_to_f32(d[2] >> 16);
-    const float x6 = bf16_to_f32(d[3] & 0xFFFFu), x7 = bf16_to_f32(d[3] >> 16);
-    float c = -136.0f * (((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)));
-    u32x4_t p;
-    p[0] = (d[0] & 0xFFFFu) | (d[2] << 16);      // (x0, x4)
-    p[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);  // (x1, x5)
-    p[2] = (d[1] & 0xFFFFu) | (d[3] << 16);      // (x2, x6)
-    p[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);  // (x3, x7)
-    if (u < n_oct + 4) xp[lds_octet(u)] = p;
-    c = quad_sum(c);  // the 4 octets of a group sit in one lane quad
-    if (u < n_oct + 4 && (tid & 3) == 0) xc[u >> 2] = c;  // -C
+    stage_octet(d, u, n_oct, xp, xc, tid);
   }
 }
 
@@ -422,6 +429,32 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
 #pragma unroll
       for (int j = 0; j < NR; ++j) asm volatile("" : "+v"(woff[j]), "+v"(soff[j]));
 
+      // Passes of at most two rows load their activation rows into registers
+      // ahead of the weights: loads return in order, so a row load issued
+      // behind the weight prefetch would make the staging below wait for the
+      // weights too, and the staging work and barrier would follow their
+      // latency instead of running under it.  (Four-row passes have no
+      // registers to spare for it.)
+      constexpr bool kEarly = NIT > 0 && NTOK <= 2;
+      constexpr int kOctMax = NIT * LPR * 4 + 4;  // row octets + the zero group
+      constexpr int kStageIt = kEarly ? (kOctMax + NT - 1) / NT : 1;
+      const int n_oct = kdim >> 3;
+      u32x4_t xs[kEarly ? NTOK : 1][kStageIt];
+      if constexpr (kEarly) {
+#pragma unroll
+        for (int t = 0; t < NTOK; ++t) {
+          const int f = slot_of(min(t0 + t, T - 1));
+          const int64_t arow = MODE == 0 ? f / a.topk : f;
+          const u32x4_t* s4 = reinterpret_cast<const u32x4_t*>(a.act + arow * a.ld_act);
+#pragma unroll
+          for (int i = 0; i < kStageIt; ++i) {
+            const int u = i * NT + tid;
+            xs[t][i] = u32x4_t{0u, 0u, 0u, 0u};
+            if (t < tc && u < n_oct) xs[t][i] = s4[u];
+          }
+        }
+      }
+
 #pragma unroll
       for (int p = 0; p < PF; ++p)
         if (NIT == 0 || p < UPW * NIT) {
@@ -431,11 +464,23 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
 
       // Stage this pass's activation rows (the whole workgroup).
       __syncthreads();
-      for (int t = 0; t < tc; ++t) {
-        const int f = slot_of(t0 + t);
-        const int64_t arow = MODE == 0 ? f / a.topk : f;
-        stage_row<NT>(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * xc_pitch,
-                      tid);
+      if constexpr (kEarly) {
+#pragma unroll
+        for (int t = 0; t < NTOK; ++t)
+          if (t < tc) {
+#pragma unroll
+            for (int i = 0; i < kStageIt; ++i)
+              if (i * NT < n_oct + 4)
+                stage_octet(xs[t][i], i * NT + tid, n_oct, xp + t * row_oct,
+                            xc + t * xc_pitch, tid);
+          }
+      } else {
+        for (int t = 0; t < tc; ++t) {
+          const int f = slot_of(t0 + t);
+          const int64_t arow = MODE == 0 ? f / a.topk : f;
+          stage_row<NT>(a.act + arow * a.ld_act, kdim, xp + t * row_oct, xc + t * xc_pitch,
+                        tid);
+        }
       }
       __syncthreads();
 
