@@ -445,6 +445,29 @@ def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
     assert mab <= MAX_ABS_MAX
 
 
+@pytest.mark.parametrize("M,skewed", [(3, False), (8, True), (16, True)])
+def test_gemv_rows_per_pass_bit_identical(pkg, synth, dev, M, skewed):
+    """A token's dot products in the GEMV run the same chain whatever the
+    number of token rows per pass.  Passes of one or two rows load their
+    activation rows ahead of the weight prefetch, passes of three or four
+    after it; an expert with four or more pairs takes four-row passes at
+    tc = 4 and one-row passes at tc = 1, so every tc gives the same bits
+    (the lanes per row fixed: they set the reduction order)."""
+    shape = synth.LayerShape(E=16, topk=4, K=3072, N=1024, group=32)
+    w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=31, skewed=skewed)
+    counts = torch.bincount(ti.reshape(-1).cpu(), minlength=shape.E)
+    if M >= 8:
+        assert int(counts.max()) >= 4  # four-row passes occur at tc = 4
+    outs = []
+    for tc in (1, 2, 4):
+        t = pkg.Tuning(gemv_only_max_m=1 << 20, gemv_max_tokens=4, gemv_tokens_per_pass=tc,
+                       gemv_lanes_per_row=8, w2_fused_max_m=1)
+        outs.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=t))
+    torch.cuda.synchronize()
+    for tc, o in zip((2, 4), outs[1:]):
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), f"tc={tc}"
+
+
 @pytest.mark.parametrize("E,topk,K,N,M,tile_m", [(256, 10, 3072, 1024, 640, 0),
                                                  (4, 2, 1024, 512, 400, 0),
                                                  (256, 10, 3072, 1024, 64, 64),
