@@ -423,6 +423,32 @@ def test_full_size_configs(pkg, orc, synth, dev, full_layer, cfg_index, dispatch
            bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K, tuning))
 
 
+@pytest.mark.parametrize("M,skewed", [(2, False), (3, True), (8, True), (24, False), (24, True),
+                                      (28, True), (48, True)])
+def test_full_size_table_entries(pkg, orc, synth, dev, full_layer, M, skewed):
+    """Every output row at full size under the committed table's entry for M
+    (nearest key): the decode and small-batch entries, which the benchmark
+    configurations do not reach (M=2-3 GEMV-only with two 32-lane rows per
+    pass, M=21-28 the split with a 2-pair threshold)."""
+    shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
+    tuning = _dispatch(pkg, "table", M, shape, dev)
+    print(f"full-size M={M} skewed={skewed} (table: {tuning})", flush=True)
+    x = synth.make_hidden(M, shape.K, dev, seed=M)
+    tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=M, skewed=skewed)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=tuning)
+    torch.cuda.synchronize()
+    # 32 lanes per weight row add a group's products in another order than
+    # the 8-lane variant (a 32-lane tree), and a one-ulp flip of a bf16
+    # intermediate value moves every output of its token a little: more
+    # outputs end one bf16 ulp from bf16(tight) (M=2: 2.75 %), all within
+    # the rounding bound checked above them.
+    flips = 0.04 if tuning.gemv_lanes_per_row == 32 else 0.02
+    _check(orc, out, x.cpu(), c13, c2, cs13, cs2, tw.cpu(), ti.cpu(), 32,
+           f"table M={M} skewed={skewed}",
+           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K, tuning),
+           mismatch_max=flips)
+
+
 def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
     """max-abs <= 2e-2 at the reference bench's magnitudes (x/10, w ~ randn/10)."""
     shape = synth.LayerShape()
