@@ -474,11 +474,11 @@ def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
 @pytest.mark.parametrize("M,skewed", [(3, False), (8, True), (16, True)])
 def test_gemv_rows_per_pass_bit_identical(pkg, synth, dev, M, skewed):
     """A token's dot products in the GEMV run the same chain whatever the
-    number of token rows per pass.  Passes of one or two rows load their
-    activation rows ahead of the weight prefetch, passes of three or four
-    after it; an expert with four or more pairs takes four-row passes at
-    tc = 4 and one-row passes at tc = 1, so every tc gives the same bits
-    (the lanes per row fixed: they set the reduction order)."""
+    number of token rows per pass.  Passes of one to three rows load their
+    activation rows ahead of the weight prefetch, four-row passes after it;
+    an expert with four or more pairs takes four-row passes at tc = 4 and
+    one-row passes at tc = 1, so every tc gives the same bits (the lanes per
+    row fixed: they set the reduction order)."""
     shape = synth.LayerShape(E=16, topk=4, K=3072, N=1024, group=32)
     w13, w2, s13, s2, x, tw, ti = _make(synth, shape, M, dev, seed=31, skewed=skewed)
     counts = torch.bincount(ti.reshape(-1).cpu(), minlength=shape.E)
