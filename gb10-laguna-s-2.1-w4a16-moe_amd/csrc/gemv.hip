@@ -59,7 +59,26 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
   const float wt = a.topk_w[f];  // loaded with the id, used at the end
   const bool valid = e_raw >= 0 && e_raw < E;  // wave-uniform
   const int e = valid ? e_raw : 0;
-  stage_row<64>(a.act + (int64_t)f * a.ld_act, kdim, xp, xc, lane);
+  // The slot's intermediate row: with the step count fixed at compile time
+  // its pieces are loaded together (one round trip instead of one per piece)
+  // and staged before the weight loads are issued.
+  if constexpr (NIT > 0) {
+    constexpr int kStageIt = (NIT * 32 + 4 + 63) / 64;  // row octets + zero group
+    const int n_oct = kdim >> 3;
+    const u32x4_t* xrow = reinterpret_cast<const u32x4_t*>(a.act + (int64_t)f * a.ld_act);
+    u32x4_t xs[kStageIt];
+#pragma unroll
+    for (int i = 0; i < kStageIt; ++i) {
+      const int u = i * 64 + lane;
+      xs[i] = u32x4_t{0u, 0u, 0u, 0u};
+      if (u < n_oct) xs[i] = xrow[u];
+    }
+#pragma unroll
+    for (int i = 0; i < kStageIt; ++i)
+      if (i * 64 < n_oct + 4) stage_octet(xs[i], i * 64 + lane, n_oct, xp, xc, lane);
+  } else {
+    stage_row<64>(a.act + (int64_t)f * a.ld_act, kdim, xp, xc, lane);
+  }
 
   // Lane (r, sl) owns rows rb0 + r + 8 j, j < R, of the workgroup's 8 R.
   const int r = lane >> 3, sl = lane & 7;
