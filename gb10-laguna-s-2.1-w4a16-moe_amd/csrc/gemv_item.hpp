@@ -429,13 +429,13 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
 #pragma unroll
       for (int j = 0; j < NR; ++j) asm volatile("" : "+v"(woff[j]), "+v"(soff[j]));
 
-      // Passes of at most three rows load their activation rows into
-      // registers ahead of the weights: loads return in order, so a row load
-      // issued behind the weight prefetch would make the staging below wait
-      // for the weights too, and the staging work and barrier would follow
-      // their latency instead of running under it.  (Four-row passes have no
-      // registers to spare for it.)
-      constexpr bool kEarly = NIT > 0 && NTOK <= 3;
+      // Passes of at most three rows (any pass of w2's short rows) load their
+      // activation rows into registers ahead of the weights: loads return in
+      // order, so a row load issued behind the weight prefetch would make the
+      // staging below wait for the weights too, and the staging work and
+      // barrier would follow their latency instead of running under it.
+      // (w13's four-row passes have no registers to spare for it.)
+      constexpr bool kEarly = NIT > 0 && (NTOK <= 3 || MODE == 1);
       constexpr int kOctMax = NIT * LPR * 4 + 4;  // row octets + the zero group
       constexpr int kStageIt = kEarly ? (kOctMax + NT - 1) / NT : 1;
       const int n_oct = kdim >> 3;
