@@ -15,9 +15,10 @@
 //      take rank = popcount(peers below me) and the lowest peer advances the
 //      wave's cursor -- ascending flat index inside an expert, as a stable
 //      sort gives;
-//   5. padding slots and the tail get the sentinel M*topk, blocks get their
-//      expert by binary search of the offsets (searchsorted right=True),
-//      blocks past the padded end get -1.
+//   5. padding slots and the tail get the sentinel M*topk, each expert's
+//      thread writes the expert id of the blocks it owns (what searchsorted
+//      right=True of the block starts over the offsets gives), blocks past
+//      the padded end get -1.
 // Integer only; the output is bit-identical to the reference over the whole
 // fixed-size buffers.  Ids outside [0, E) are skipped and counted.
 #include "common.hpp"
@@ -151,6 +152,20 @@ __device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const
   }
 }
 
+// Block b's expert (-1 past the padded total): expert e owns blocks
+// off[e] / B .. off[e+1] / B - 1 (the offsets are multiples of B), so each
+// expert's thread writes its own -- the searchsorted(right) of the
+// reference's block starts over the offsets, without a search per block.
+__device__ void write_expert_ids(const AlignLaunch& a, const int32_t* off, int total, int tid,
+                                 int nthr) {
+  const int B = a.block;
+  for (int e = tid; e < a.num_experts; e += nthr) {
+    const int b1 = min(off[e + 1] / B, a.n_blocks);
+    for (int b = off[e] / B; b < b1; ++b) a.expert_ids[b] = e;
+  }
+  for (int b = total / B + tid; b < a.n_blocks; b += nthr) a.expert_ids[b] = -1;
+}
+
 __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   extern __shared__ int32_t smem[];
   __shared__ int32_t wave_tot[17];
@@ -191,11 +206,25 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
     }
   };
 
+  // A wave's share of at most one batch (every call below the many-workgroup
+  // sort's size) is loaded once and kept in registers for the placement.  A
+  // wave with no ids loads nothing (with no pairs at all the id buffer is
+  // empty, and load_batch's clamped index would still read entry 0); its
+  // loops below do not run.
+  const bool one_batch = end - beg <= 64 * kBatch;  // uniform
+  int ev1[kBatch];
+  if (one_batch && beg < end) load_batch(beg, ev1);
+
   // 1. per-wave histogram
   int drop = 0;
   for (int f0 = beg; f0 < end; f0 += 64 * kBatch) {
     int ev[kBatch];
-    load_batch(f0, ev);
+    if (one_batch) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) ev[u] = ev1[u];
+    } else {
+      load_batch(f0, ev);
+    }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (f0 + 64 * u >= end) break;  // uniform
@@ -256,7 +285,12 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   const uint64_t lt = lanemask_lt();
   for (int fb = beg; fb < end; fb += 64 * kBatch) {
     int ev[kBatch];
-    load_batch(fb, ev);
+    if (one_batch) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) ev[u] = ev1[u];
+    } else {
+      load_batch(fb, ev);
+    }
     // the 64-id groups in ascending order: each advances the wave's cursors
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -288,22 +322,7 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
     for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
   }
   for (int p = total + tid; p < a.em; p += nthr) a.sorted[p] = n_tok;
-  for (int b = tid; b < a.n_blocks; b += nthr) {
-    int eid = -1;
-    const int pos = b * B;
-    if (pos < total) {
-      int lo = 0, hi = E - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (off[mid + 1] > pos)
-          hi = mid;
-        else
-          lo = mid + 1;
-      }
-      eid = lo;
-    }
-    a.expert_ids[b] = eid;
-  }
+  write_expert_ids(a, off, total, tid, nthr);
   if (a.offsets)
     for (int e = tid; e <= E; e += nthr) a.offsets[e] = off[e];
   if (tid == 0) {
@@ -454,22 +473,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
     for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
   }
   for (int p = total + tid; p < a.em; p += kChunk) a.sorted[p] = n_tok;
-  for (int b = tid; b < a.n_blocks; b += kChunk) {
-    int eid = -1;
-    const int pos = b * B;
-    if (pos < total) {
-      int lo = 0, hi = E - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (off[mid + 1] > pos)
-          hi = mid;
-        else
-          lo = mid + 1;
-      }
-      eid = lo;
-    }
-    a.expert_ids[b] = eid;
-  }
+  write_expert_ids(a, off, total, tid, kChunk);
   if (a.offsets)
     for (int e = tid; e <= E; e += kChunk) a.offsets[e] = off[e];
   if (tid == 0) {
