@@ -225,9 +225,9 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
 //
 // `bid` is the workgroup's index in the launch's GEMV range (its block index
 // in a GEMV-only launch) and `lds` the workgroup's dynamic LDS.
-template <int MODE, int RPL, int PF, int TC, int WAVES, int NIT, bool ROUTE, int UPW, int LPR>
+template <int MODE, int RPL, int PF_, int TC, int WAVES, int NIT, bool ROUTE, int UPW, int LPR>
 __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* lds) {
-  static_assert(UPW == 1 || (NIT > 0 && NIT % PF == 0), "units per workgroup need unrolled steps");
+  static_assert(UPW == 1 || (NIT > 0 && NIT % PF_ == 0), "units per workgroup need unrolled steps");
   static_assert(LPR == 8 || LPR == 16 || LPR == 32, "lanes per row");
   constexpr int NR = MODE == 0 ? 2 * RPL : RPL;  // weight rows per lane
   constexpr int NT = 64 * WAVES;
@@ -340,6 +340,10 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
   // flight across a loop edge, so every wait the compiler places is exact.
   auto body = [&](auto ntok_c) {
     constexpr int NTOK = decltype(ntok_c)::value;
+    // w13's four-row passes keep one step less in flight: the registers pay
+    // for loading each activation row's pieces together (below).
+    constexpr bool kRowBatch = MODE == 0 && NTOK == 4 && NIT > 0 && PF_ > 3 && NIT % 3 == 0;
+    constexpr int PF = kRowBatch ? 3 : PF_;
     // Weight and raw bf16 scale registers of PF steps in flight.  Scales
     // stay as raw bits until use: converting right after the load would make
     // the compiler wait for it there and serialise the prefetch ring.
@@ -474,6 +478,26 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
                 stage_octet(xs[t][i], i * NT + tid, n_oct, xp + t * row_oct,
                             xc + t * xc_pitch, tid);
           }
+      } else if constexpr (kRowBatch) {
+        // A row's pieces are loaded together: one round trip per row instead
+        // of one per piece.
+        constexpr int kRowIt = (kOctMax + NT - 1) / NT;
+        for (int t = 0; t < tc; ++t) {
+          const int f = slot_of(t0 + t);
+          const int64_t arow = MODE == 0 ? f / a.topk : f;
+          const u32x4_t* s4 = reinterpret_cast<const u32x4_t*>(a.act + arow * a.ld_act);
+          u32x4_t xr[kRowIt];
+#pragma unroll
+          for (int i = 0; i < kRowIt; ++i) {
+            const int u = i * NT + tid;
+            xr[i] = u32x4_t{0u, 0u, 0u, 0u};
+            if (u < n_oct) xr[i] = s4[u];
+          }
+#pragma unroll
+          for (int i = 0; i < kRowIt; ++i)
+            if (i * NT < n_oct + 4)
+              stage_octet(xr[i], i * NT + tid, n_oct, xp + t * row_oct, xc + t * xc_pitch, tid);
+        }
       } else {
         for (int t = 0; t < tc; ++t) {
           const int f = slot_of(t0 + t);
