@@ -623,7 +623,7 @@ size_t gemv_lds_bytes(int tc, int kdim) {
 #define W4A16_W2_RPL 2
 #endif
 #ifndef W4A16_W2_PF
-#define W4A16_W2_PF 2
+#define W4A16_W2_PF 4
 #endif
 
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts
