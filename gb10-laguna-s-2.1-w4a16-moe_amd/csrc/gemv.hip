@@ -266,7 +266,9 @@ hipError_t launch_gemv_t(const GemvLaunch& a, hipStream_t stream) {
 
 
 
-template <int MODE, int R, int P>
+// R, P: rows per lane and steps in flight of passes of one or two token
+// rows; R4, P4: those of four-row passes.
+template <int MODE, int R, int P, int R4 = R, int P4 = P>
 hipError_t launch_gemv_tc(const GemvLaunch& a, hipStream_t stream) {
   const int tc = pick_tc(a, a.num_experts);
   const bool wide = pick_lpr(a, tc, MODE) == 32;
@@ -275,7 +277,7 @@ hipError_t launch_gemv_tc(const GemvLaunch& a, hipStream_t stream) {
                         : launch_gemv_t<MODE, R, P, 1>(a, stream);
     case 2: return wide ? launch_gemv_t<MODE, R, P, 2, 32>(a, stream)
                         : launch_gemv_t<MODE, R, P, 2>(a, stream);
-    default: return launch_gemv_t<MODE, R, P, 4>(a, stream);
+    default: return launch_gemv_t<MODE, R4, P4, 4>(a, stream);
   }
 }
 
@@ -322,7 +324,7 @@ hipError_t launch_w2_gemv(const GemvLaunch& a_in, hipStream_t stream) {
   GemvLaunch a = a_in;
   a.nib_mask = 0x000F000Fu;
   a.nib_magic = 0x43004300u;
-  return launch_gemv_tc<1, W4A16_W2_RPL, W4A16_W2_PF>(a, stream);
+  return launch_gemv_tc<1, W4A16_W2_RPL, W4A16_W2_PF, W4A16_W2_RPL_T4, W4A16_W2_PF_T4>(a, stream);
 }
 
 }  // namespace w4a16

@@ -612,7 +612,12 @@ size_t gemv_lds_bytes(int tc, int kdim) {
 }
 
 // Launch shapes: output rows per lane (RPL) and prefetch depth (PF) of the
-// two GEMVs, waves per workgroup.  Overridable at build time for tuning sweeps.
+// two GEMVs, waves per workgroup.  w2's passes of four token rows have their
+// own shape (_T4): 4 rows per lane with 2 steps in flight moves the same
+// weight bytes per lane as 2 rows with 4 steps, in half the workgroups, and
+// measured faster there (skewed M=64 133.6 -> 131.7 us, uniform M=32 203.1
+// -> 198.7 us per call) but slower for passes of one or two rows.
+// Overridable at build time for tuning sweeps.
 #ifndef W4A16_W13_RPL
 #define W4A16_W13_RPL 1
 #endif
@@ -624,6 +629,12 @@ size_t gemv_lds_bytes(int tc, int kdim) {
 #endif
 #ifndef W4A16_W2_PF
 #define W4A16_W2_PF 4
+#endif
+#ifndef W4A16_W2_RPL_T4
+#define W4A16_W2_RPL_T4 4
+#endif
+#ifndef W4A16_W2_PF_T4
+#define W4A16_W2_PF_T4 2
 #endif
 
 // M == 1 routes one pair per expert; up to M*topk <= E most touched experts

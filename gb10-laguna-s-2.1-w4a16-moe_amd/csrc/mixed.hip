@@ -51,6 +51,11 @@ void mixed_kernel(const MfmaLaunch m, const GemvLaunch g) {
 constexpr int kNitW13 = 12;
 constexpr int kNitW2 = 4;
 
+// GEMV output rows per lane of the mixed kernels, by token rows per pass.
+constexpr int mixed_rpl(int mode, int tc) {
+  return mode == 0 ? W4A16_W13_RPL : (tc == 4 ? W4A16_W2_RPL_T4 : W4A16_W2_RPL);
+}
+
 // Token rows per GEMV pass the call would use, or 0 when no mixed kernel
 // covers its GEMV launch.
 int mixed_tc(int mode, const MfmaLaunch& m, const GemvLaunch& g) {
@@ -62,42 +67,44 @@ int mixed_tc(int mode, const MfmaLaunch& m, const GemvLaunch& g) {
   if ((tc != 2 && tc != 4) || pick_lpr(g, tc, mode) != 8 || g.upw > 1 || g.ids || !g.block_list)
     return 0;
   if (((g.kdim >> 5) + 7) / 8 != (mode == 0 ? kNitW13 : kNitW2)) return 0;
-  const int rpl = mode == 0 ? W4A16_W13_RPL : W4A16_W2_RPL;
-  if (g.n_out % (8 * rpl) != 0) return 0;
+  if (g.n_out % (8 * mixed_rpl(mode, tc)) != 0) return 0;
   if (m.group != 32 && m.group != 64 && m.group != 128) return 0;
   return tc;
 }
 
-template <int MODE, int RPL, int PF, int NIT>
+// RPL, PF: GEMV rows per lane and steps in flight of two-row passes; RPL4,
+// PF4: those of four-row passes.
+template <int MODE, int RPL, int PF, int RPL4, int PF4, int NIT>
 hipError_t launch_mixed_t(const MfmaLaunch& m, const GemvLaunch& g_in, hipStream_t stream) {
   using namespace gemv_dev;
   static_assert(kGemvWaves == SmallTile::kWaves, "GEMV and MFMA workgroups of one size");
+  static_assert(mixed_rpl(MODE, 2) == RPL && mixed_rpl(MODE, 4) == RPL4, "rows per lane");
   const int tc = mixed_tc(MODE, m, g_in);
   if (tc == 0) return hipErrorInvalidValue;
   GemvLaunch g = g_in;
   g.nib_mask = 0x000F000Fu;
   g.nib_magic = 0x43004300u;  // bf16 (128, 128)
-  const int chunks = g.n_out / (8 * RPL);
+  const int chunks = g.n_out / (8 * (tc == 4 ? RPL4 : RPL));
   const int groups = (chunks + kGemvWaves - 1) / kGemvWaves;
   const int64_t grid = mfma_dev::mfma_grid<MODE, SmallTile>(m) + (int64_t)g.max_blocks * groups;
   if (grid <= 0) return hipSuccess;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
   const size_t lds = std::max<size_t>(SmallTile::kLdsTotal, gemv_lds_bytes(tc, g.kdim));
   const dim3 gr((unsigned)grid), b(SmallTile::kWaves * 64);
-#define W4A16_MIXED(GS, TC_)                                                                  \
-  hipLaunchKernelGGL((mixed_kernel<MODE, GS, RPL, PF, TC_, NIT>), gr, b, lds, stream, m, g); \
+#define W4A16_MIXED(GS, R_, P_, TC_)                                                         \
+  hipLaunchKernelGGL((mixed_kernel<MODE, GS, R_, P_, TC_, NIT>), gr, b, lds, stream, m, g); \
   break;
   if (tc == 4) {
     switch (m.group) {
-      case 32: W4A16_MIXED(0, 4)
-      case 64: W4A16_MIXED(1, 4)
-      default: W4A16_MIXED(2, 4)
+      case 32: W4A16_MIXED(0, RPL4, PF4, 4)
+      case 64: W4A16_MIXED(1, RPL4, PF4, 4)
+      default: W4A16_MIXED(2, RPL4, PF4, 4)
     }
   } else {
     switch (m.group) {
-      case 32: W4A16_MIXED(0, 2)
-      case 64: W4A16_MIXED(1, 2)
-      default: W4A16_MIXED(2, 2)
+      case 32: W4A16_MIXED(0, RPL, PF, 2)
+      case 64: W4A16_MIXED(1, RPL, PF, 2)
+      default: W4A16_MIXED(2, RPL, PF, 2)
     }
   }
 #undef W4A16_MIXED
@@ -111,11 +118,13 @@ bool mixed_fits(int mode, const MfmaLaunch& m, const GemvLaunch& g) {
 }
 
 hipError_t launch_w13_mixed(const MfmaLaunch& m, const GemvLaunch& g, hipStream_t stream) {
-  return launch_mixed_t<0, W4A16_W13_RPL, W4A16_W13_PF, kNitW13>(m, g, stream);
+  return launch_mixed_t<0, W4A16_W13_RPL, W4A16_W13_PF, W4A16_W13_RPL, W4A16_W13_PF, kNitW13>(
+      m, g, stream);
 }
 
 hipError_t launch_w2_mixed(const MfmaLaunch& m, const GemvLaunch& g, hipStream_t stream) {
-  return launch_mixed_t<1, W4A16_W2_RPL, W4A16_W2_PF, kNitW2>(m, g, stream);
+  return launch_mixed_t<1, W4A16_W2_RPL, W4A16_W2_PF, W4A16_W2_RPL_T4, W4A16_W2_PF_T4, kNitW2>(
+      m, g, stream);
 }
 
 }  // namespace w4a16
