@@ -285,7 +285,8 @@ hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
   GemvLaunch a = a_in;
   a.nib_mask = 0x000F000Fu;
   a.nib_magic = 0x43004300u;  // bf16 (128, 128)
-  return launch_gemv_tc<0, W4A16_W13_RPL, W4A16_W13_PF>(a, stream);
+  return launch_gemv_tc<0, W4A16_W13_RPL, W4A16_W13_PF, W4A16_W13_RPL_T4, W4A16_W13_PF_T4>(a,
+                                                                                       stream);
 }
 
 bool gemv_route_fits(int n_tok, int num_experts, int K, int N) {

@@ -630,6 +630,12 @@ size_t gemv_lds_bytes(int tc, int kdim) {
 #ifndef W4A16_W2_PF
 #define W4A16_W2_PF 4
 #endif
+#ifndef W4A16_W13_RPL_T4
+#define W4A16_W13_RPL_T4 W4A16_W13_RPL
+#endif
+#ifndef W4A16_W13_PF_T4
+#define W4A16_W13_PF_T4 W4A16_W13_PF
+#endif
 #ifndef W4A16_W2_RPL_T4
 #define W4A16_W2_RPL_T4 4
 #endif

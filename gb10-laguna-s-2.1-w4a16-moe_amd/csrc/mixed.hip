@@ -53,7 +53,8 @@ constexpr int kNitW2 = 4;
 
 // GEMV output rows per lane of the mixed kernels, by token rows per pass.
 constexpr int mixed_rpl(int mode, int tc) {
-  return mode == 0 ? W4A16_W13_RPL : (tc == 4 ? W4A16_W2_RPL_T4 : W4A16_W2_RPL);
+  return mode == 0 ? (tc == 4 ? W4A16_W13_RPL_T4 : W4A16_W13_RPL)
+                   : (tc == 4 ? W4A16_W2_RPL_T4 : W4A16_W2_RPL);
 }
 
 // Token rows per GEMV pass the call would use, or 0 when no mixed kernel
@@ -118,8 +119,8 @@ bool mixed_fits(int mode, const MfmaLaunch& m, const GemvLaunch& g) {
 }
 
 hipError_t launch_w13_mixed(const MfmaLaunch& m, const GemvLaunch& g, hipStream_t stream) {
-  return launch_mixed_t<0, W4A16_W13_RPL, W4A16_W13_PF, W4A16_W13_RPL, W4A16_W13_PF, kNitW13>(
-      m, g, stream);
+  return launch_mixed_t<0, W4A16_W13_RPL, W4A16_W13_PF, W4A16_W13_RPL_T4, W4A16_W13_PF_T4,
+                        kNitW13>(m, g, stream);
 }
 
 hipError_t launch_w2_mixed(const MfmaLaunch& m, const GemvLaunch& g, hipStream_t stream) {
