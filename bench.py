@@ -363,6 +363,17 @@ def parity_row(wl, cpu_budget_s, max_calls=9):
     }
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (Linux /proc/cpuinfo), else the architecture."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
     """Time the oracle's CPU dequant reference on set 0 of the workload."""
     import torch
@@ -394,7 +405,8 @@ def cpu_baseline(wl, seconds_target=15.0, max_iters=10):
                    f"1 warmup + {len(timed)} timed calls, p50 {p50 * 1e3:.1f} ms; each "
                    f"config row's \"cpu\" field times the same reference on that config "
                    f"(config 0, M=1, is the one BASELINE.md names)"),
-        "cpu": platform.processor() or platform.machine(),
+        "cpu": cpu_model(),
+        "host_cpus": os.cpu_count(),
         "gpu_vs_cpu_rel_l2": orc.rel_l2(gpu_out, ref32),
         "gpu_vs_cpu_max_abs": orc.max_abs(gpu_out, ref32),
     }
