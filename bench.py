@@ -175,6 +175,7 @@ class Workload:
         p50 = sorted(per)[len(per) // 2]
         nbytes = sum(self.bytes[i % n] for c in chunks for i in range(c))
         del graphs
+        self.pkg.release_graph_workspaces()
         return {"elapsed_ms": p50, "wall_s": wall, "steps": steps, "bytes": nbytes,
                 "replays": replays, "warmup_replays": n_warm,
                 "replay_ms": {"p50": round(p50, 4), "min": round(min(per), 4),

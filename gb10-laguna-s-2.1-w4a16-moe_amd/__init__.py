@@ -16,6 +16,7 @@ from .w4a16_moe import (  # noqa: F401
     is_repacked,
     moe_align_block_size,
     moe_align_block_size_full,
+    release_graph_workspaces,
     repack_weights,
     workspace_tensor,
 )

@@ -27,6 +27,7 @@ W4A16_ERR_HIP = 7
 W4A16_ERR_UNSUPPORTED_DTYPE = 8
 W4A16_ERR_INVALID_TUNING = 9
 W4A16_ERR_SCRATCH_TOO_SMALL = 10
+W4A16_ERR_WRONG_DEVICE = 11
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 LOGITS_F32 = 0
@@ -56,6 +57,7 @@ EXPORTED_SYMBOLS = (
     "w4a16_moe_fused_experts_profiled",
     "w4a16_moe_run_stage",
     "w4a16_moe_dropped_pairs",
+    "w4a16_moe_capture_id",
     "w4a16_moe_router_topk_softmax",
     "w4a16_moe_default_tuning",
     "w4a16_moe_workspace_size_ex",
@@ -114,6 +116,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.w4a16_moe_run_stage.argtypes = [ctypes.c_int] + fused
     lib.w4a16_moe_dropped_pairs.restype = ctypes.c_int
     lib.w4a16_moe_dropped_pairs.argtypes = [_vp, ctypes.POINTER(ctypes.c_int32), _vp]
+    lib.w4a16_moe_capture_id.restype = ctypes.c_int
+    lib.w4a16_moe_capture_id.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint64)]
     tp = ctypes.POINTER(TuningStruct)
     lib.w4a16_moe_default_tuning.restype = ctypes.c_int
     lib.w4a16_moe_default_tuning.argtypes = [_i64] * 6 + [tp]
@@ -219,6 +223,14 @@ class W4A16Error(AssertionError, ValueError):
 
 class W4A16RuntimeError(RuntimeError):
     """The HIP runtime reported a failure."""
+
+
+def capture_id(stream: int) -> int:
+    """0 when `stream` is not being captured into a HIP graph, else the id of
+    the capture in progress."""
+    out = ctypes.c_uint64()
+    check(lib().w4a16_moe_capture_id(stream, ctypes.byref(out)))
+    return int(out.value)
 
 
 def check(status: int) -> None:

@@ -547,7 +547,8 @@ int scratch_for(hipStream_t stream, void** out) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return W4A16_ERR_HIP;
   if (stream) {
     hipDevice_t sdev = -1;
-    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) return W4A16_ERR_HIP;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) return W4A16_ERR_HIP;
+    if (sdev != dev) return W4A16_ERR_WRONG_DEVICE;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
@@ -581,6 +582,8 @@ const char* w4a16_moe_strerror(int status) {
     case W4A16_ERR_SCRATCH_TOO_SMALL:
       return "call needs more workspace than the static scratch of the allocation-free "
              "entry point holds";
+    case W4A16_ERR_WRONG_DEVICE:
+      return "the stream's device is not the current device";
     default: return "unknown status";
   }
 }
@@ -821,12 +824,16 @@ int w4a16_moe_fused_experts_noalloc(const void* hidden, int64_t ld_hidden,
                                     int64_t K, int64_t group_size, void* out, int64_t ld_out,
                                     void* stream, const w4a16_moe_tuning* tuning) {
   // The size check comes first: it needs no device and rejects a call too
-  // big for the scratch before anything else runs.
+  // big for the scratch before anything else runs.  The layout is the one
+  // validate() builds for these pointers (the MFMA kernels need 16-byte
+  // aligned scales; without them every expert runs on the GEMV kernels,
+  // whose work lists are sized differently).
   Tuning T;
   int st = resolve_tuning(tuning, &T);
   if (st) return st;
   Layout L;
-  st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L);
+  st = compute_layout(M, topk, num_experts, N, K, group_size, T, &L,
+                      aligned(w13_scale, 16) && aligned(w2_scale, 16));
   if (st) return st;
   if (M == 0) return W4A16_OK;
   if (L.total > kNoallocScratchBytes) return W4A16_ERR_SCRATCH_TOO_SMALL;
@@ -838,8 +845,19 @@ int w4a16_moe_fused_experts_noalloc(const void* hidden, int64_t ld_hidden,
                     topk_weights, topk_ids, M, topk, num_experts, N, K, group_size,
                     out, ld_out, ws, kNoallocScratchBytes, tuning};
   st = validate(a, &L);
+  if (st == W4A16_ERR_WORKSPACE_TOO_SMALL) return W4A16_ERR_SCRATCH_TOO_SMALL;
   if (st) return st;
   return run_fused(a, L, s, nullptr);
+}
+
+int w4a16_moe_capture_id(void* stream, uint64_t* capture_id) {
+  if (!capture_id) return W4A16_ERR_NULL_POINTER;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  if (hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &id) != hipSuccess)
+    return W4A16_ERR_HIP;
+  *capture_id = status == hipStreamCaptureStatusActive ? (uint64_t)id : 0;
+  return W4A16_OK;
 }
 
 int w4a16_moe_dropped_pairs(const void* workspace, int32_t* count, void* stream) {

@@ -37,57 +37,89 @@ BLOCK_K = 64
 
 
 class WorkspacePool:
-    """Workspaces of the fused call: one buffer per (device, stream), grown to
-    the largest size a call has needed and reused by every smaller call.
+    """Workspaces of the fused call, kept for reuse.
+
+    Eager calls: one buffer per (device, stream), grown to the largest size a
+    call has needed and reused by every smaller call.  Calls on one stream run
+    in order, so they can share one buffer; calls on different streams get
+    different buffers (the C ABI's rule: calls sharing a workspace must not
+    overlap).
+
+    Calls under HIP graph capture: one buffer per (device, stream, capture),
+    shared only by the calls of that capture (which the graph runs in order).
+    A graph runs on whatever stream it is replayed on, so graphs captured on
+    one stream may later run concurrently; giving each capture its own buffer
+    keeps them apart.  Capture buffers are never reused by later calls, and a
+    capture buffer outgrown within its capture stays alive (the graph's
+    kernels keep its address): both are held until ``release_captures()``
+    (or ``clear()``), which callers make once the graphs are destroyed.
 
     The reference pools its scratch per (device, M, ...) shape
     (kernels/w4a16_moe.py:293-316), which keeps one buffer per distinct M for
-    the life of the process.  Calls on one stream run in order, so they can
-    share one buffer; calls on different streams get different buffers (the
-    C ABI's rule: calls sharing a workspace must not overlap).  A buffer that
-    a HIP graph captured stays alive when the pool grows past it, since the
-    graph's kernels keep its address.
+    the life of the process.
     """
 
     def __init__(self, alloc=None):
         self._alloc = alloc or (lambda nbytes, device: torch.empty(
             nbytes, dtype=torch.uint8, device=device))
         self._bufs: dict[tuple, torch.Tensor] = {}
-        self._captured: set[tuple] = set()
-        self._retired: list[torch.Tensor] = []  # captured buffers outgrown
+        self._retired: list[torch.Tensor] = []  # capture buffers outgrown in their capture
         self._lock = threading.Lock()
 
-    def get(self, device, stream: int, nbytes: int, capturing: bool = False) -> torch.Tensor:
-        key = (str(device), int(stream))
+    def get(self, device, stream: int, nbytes: int, capture_id: int = 0) -> torch.Tensor:
+        """A workspace of at least `nbytes` for a call on `stream`, under the
+        graph capture `capture_id` (0: not capturing)."""
+        key = (str(device), int(stream), int(capture_id))
         need = max(int(nbytes), 256)
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < need:
-                if buf is not None and key in self._captured:
+                if buf is not None and capture_id:
                     self._retired.append(buf)
-                self._captured.discard(key)
                 buf = self._alloc(need, device)
                 self._bufs[key] = buf
-            if capturing:
-                self._captured.add(key)
             return buf
 
     def cached_bytes(self) -> int:
-        """Bytes held by the live buffers (retired captured ones excluded)."""
+        """Bytes held by the live buffers (eager and capture ones)."""
         return sum(b.numel() for b in self._bufs.values())
 
+    def capture_bytes(self) -> int:
+        """Bytes held for graph captures (live and outgrown)."""
+        return (sum(b.numel() for k, b in self._bufs.items() if k[2])
+                + sum(b.numel() for b in self._retired))
+
     def retired_bytes(self) -> int:
+        """Bytes of capture buffers outgrown within their capture (held until
+        ``release_captures()``)."""
         return sum(b.numel() for b in self._retired)
+
+    def release_captures(self) -> None:
+        """Drop every capture buffer; only once the graphs that captured them
+        are destroyed.  The eager buffers stay."""
+        with self._lock:
+            self._bufs = {k: b for k, b in self._bufs.items() if not k[2]}
+            self._retired.clear()
 
     def clear(self) -> None:
         """Drop every buffer; only for callers whose graphs are all gone."""
         with self._lock:
             self._bufs.clear()
-            self._captured.clear()
             self._retired.clear()
 
 
 _WS_POOL = WorkspacePool()
+
+
+def release_graph_workspaces() -> None:
+    """Free the workspaces held for HIP-graph captures of fused_experts_w4a16.
+
+    Each captured graph keeps its own workspace (graphs captured on one stream
+    may be replayed concurrently); call this once those graphs are destroyed.
+    Eager calls' workspaces are kept.  No counterpart in the reference, whose
+    per-shape scratch is never freed (kernels/w4a16_moe.py:293-316).
+    """
+    _WS_POOL.release_captures()
 
 
 def _fail(msg: str) -> None:
@@ -206,8 +238,8 @@ def _workspace(device: torch.device, M: int, topk: int, E: int, N: int, K: int,
     ts = None if tuning is None else tuning.to_struct()
     nbytes = _lib.workspace_size_ex(M, topk, E, N, K, group, ts)
     stream = _stream_ptr(device)
-    return _WS_POOL.get(device, stream, nbytes,
-                        capturing=torch.cuda.is_current_stream_capturing())
+    cap = _lib.capture_id(stream) if torch.cuda.is_current_stream_capturing() else 0
+    return _WS_POOL.get(device, stream, nbytes, capture_id=cap)
 
 
 class _Prepared:

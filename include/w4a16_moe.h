@@ -54,6 +54,9 @@ extern "C" {
 #define W4A16_ERR_INVALID_TUNING      9  /* a w4a16_moe_tuning field out of range */
 #define W4A16_ERR_SCRATCH_TOO_SMALL  10  /* call too big for the static scratch of
                                             w4a16_moe_fused_experts_noalloc    */
+#define W4A16_ERR_WRONG_DEVICE       11  /* w4a16_moe_fused_experts_noalloc: the
+                                            stream's device is not the current
+                                            device                            */
 
 /* Indices of w4a16_moe_workspace_layout()'s offsets array. */
 #define W4A16_WS_SORTED_IDS   0  /* int32 [EM]            sorted token-slot ids   */
@@ -192,6 +195,16 @@ int w4a16_moe_run_stage(int stage, const void* hidden, int64_t ld_hidden,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The capture sequence of `stream`: *capture_id = 0 when the stream is not
+ * being captured into a HIP graph, else the runtime's id of the capture in
+ * progress (hipStreamGetCaptureInfo).  Lets a host-side workspace pool give
+ * each captured graph its own workspace.  No GPU work, no synchronisation.
+ * Host helper; no counterpart in the reference, which pools its scratch per
+ * shape (kernels/w4a16_moe.py:293-316).
+ */
+int w4a16_moe_capture_id(void* stream, uint64_t* capture_id);
+
+/*
  * Read the dropped-pair counter the last fused call left in `workspace`
  * (waits for `stream`).  No counterpart in the reference, which has no range
  * check on topk_ids.
@@ -311,8 +324,9 @@ int w4a16_moe_fused_experts_ex(const void* hidden, int64_t ld_hidden,
  *   - Calls whose workspace (w4a16_moe_workspace_size_ex) exceeds the scratch
  *     return W4A16_ERR_SCRATCH_TOO_SMALL before any GPU work (at E=256,
  *     top-10, K=3072, N=1024 the limit is M <= 818).
- *   - `stream`'s device must be the current device.  The first call on a
- *     device resolves the scratch's address there (outside graph capture).
+ *   - `stream`'s device must be the current device (W4A16_ERR_WRONG_DEVICE
+ *     otherwise, before any GPU work).  The first call on a device resolves
+ *     the scratch's address there (outside graph capture).
  *   - Every call on one device shares that device's scratch and keeps the
  *     last call's contents: calls that overlap on one device (two streams,
  *     two host threads, two graphs replayed concurrently) race.

@@ -33,8 +33,8 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 def test_abi_version_and_strerror(lib, pkg):
     assert lib.w4a16_moe_abi_version() == 1
-    for code in range(9):
-        assert pkg._lib.strerror(code)
+    for code in range(12):
+        assert pkg._lib.strerror(code) != "unknown status", code
     assert pkg._lib.strerror(99) == "unknown status"
 
 
@@ -228,8 +228,10 @@ def test_workspace_layout_ex_follows_tuning(pkg):
 
 def test_workspace_pool_holds_one_buffer_of_the_largest_need(pkg):
     """Fifty distinct M values on one stream keep one buffer, of the largest
-    call's size; another stream gets its own; a buffer a graph captured is
-    kept (retired) when the pool grows past it."""
+    call's size; another stream gets its own; each graph capture gets a
+    buffer of its own (never the stream's eager one, never another
+    capture's), and a capture buffer outgrown within its capture is kept
+    (retired) until the captures are released."""
     import random
 
     import torch
@@ -246,9 +248,44 @@ def test_workspace_pool_holds_one_buffer_of_the_largest_need(pkg):
     assert pool.retired_bytes() == 0
     pool.get("cuda:0", 9, size[Ms[0]])
     assert pool.cached_bytes() == max(size.values()) + size[Ms[0]]
-    # a captured buffer outgrown by a later call stays alive
-    captured = pool.get("cuda:0", 11, 1000, capturing=True)
-    pool.get("cuda:0", 11, 5000)
-    assert pool.retired_bytes() == captured.numel() == 1000
+    eager = pool.get("cuda:0", 11, 4000)
+    # two captures on the same stream: distinct buffers, not the eager one
+    cap_a = pool.get("cuda:0", 11, 1000, capture_id=5)
+    cap_b = pool.get("cuda:0", 11, 1000, capture_id=6)
+    ptrs = {eager.data_ptr(), cap_a.data_ptr(), cap_b.data_ptr()}
+    assert len(ptrs) == 3
+    # calls of one capture share its buffer; the eager stream keeps its own
+    assert pool.get("cuda:0", 11, 800, capture_id=5).data_ptr() == cap_a.data_ptr()
+    assert pool.get("cuda:0", 11, 100).data_ptr() == eager.data_ptr()
+    # a capture buffer outgrown within its capture stays alive
+    grown = pool.get("cuda:0", 11, 5000, capture_id=5)
+    assert grown.data_ptr() not in ptrs
+    assert pool.retired_bytes() == cap_a.numel() == 1000
+    assert pool.capture_bytes() == 1000 + 5000 + 1000
+    live = pool.cached_bytes()
+    pool.release_captures()
+    assert pool.retired_bytes() == 0 and pool.capture_bytes() == 0
+    assert pool.cached_bytes() == live - 6000
+    assert pool.get("cuda:0", 11, 100).data_ptr() == eager.data_ptr()
     pool.clear()
     assert pool.cached_bytes() == 0 and pool.retired_bytes() == 0
+
+
+@pytest.mark.gpu
+def test_capture_id_tells_captures_apart(pkg):
+    """0 outside capture; during capture a nonzero id, different for two
+    captures of the same stream."""
+    import torch
+
+    L = pkg._lib
+    s = torch.cuda.Stream()
+    assert L.capture_id(s.cuda_stream) == 0
+    ids = []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ids.append(L.capture_id(s.cuda_stream))
+            torch.zeros(4, device="cuda").add_(1)
+        del g
+    assert ids[0] != 0 and ids[1] != 0 and ids[0] != ids[1]
+    assert L.capture_id(s.cuda_stream) == 0

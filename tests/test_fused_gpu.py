@@ -379,6 +379,44 @@ def test_graph_capture_replay(pkg, synth, dev, M):
         assert torch.equal(gout.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
 
 
+def test_graphs_captured_on_one_stream_replay_concurrently(pkg, synth, dev):
+    """Two graphs of different M captured on the same stream, then replayed at
+    the same time on two other streams: each capture holds its own workspace,
+    so both replays give the eager outputs bit for bit."""
+    shape = synth.LayerShape(E=16, topk=4, K=512, N=256, group=32)
+    w13, w2, s13, s2 = synth.make_weights(shape, dev, seed=12)
+    Ms = (260, 40)
+    ins, eager = [], []
+    for i, M in enumerate(Ms):
+        x = synth.make_hidden(M, shape.K, dev, seed=50 + i)
+        tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=50 + i)
+        ins.append((x, tw, ti))
+        eager.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32))
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    graphs, gouts = [], []
+    for x, tw, ti in ins:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            gouts.append(pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32))
+        graphs.append(g)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for r in range(4):
+        for o in gouts:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"concurrent replay {r}", flush=True)
+        for g, st in zip(graphs, streams):
+            with torch.cuda.stream(st):
+                for _ in range(3):
+                    g.replay()
+        torch.cuda.synchronize()
+        for o, e, M in zip(gouts, eager, Ms):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {r} M={M}"
+    del graphs
+    pkg.release_graph_workspaces()
+
+
 # ---- full-size layer (E=256, top-10, K=3072, N=1024, group 32) --------------
 
 
@@ -469,6 +507,69 @@ def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
     rl2, mab = _check(orc, out, x.cpu(), w13.cpu(), w2.cpu(), s13.cpu(), s2.cpu(),
                       tw.cpu(), ti.cpu(), 32, "reference magnitudes")
     assert mab <= MAX_ABS_MAX
+
+
+@pytest.fixture(scope="module")
+def ref_magnitude_layer(synth, dev):
+    """The full-size layer at the reference bench's magnitudes (weights
+    quantized from randn/10: scales ~ 0.02-0.035), on the GPU and the CPU."""
+    shape = synth.LayerShape()
+    g = torch.Generator(device=dev)
+    g.manual_seed(23)
+    E, K, N = shape.E, shape.K, shape.N
+    w13 = torch.randint(0, 256, (E, 2 * N, K // 2), generator=g, device=dev,
+                        dtype=torch.uint8)
+    w2 = torch.randint(0, 256, (E, K, N // 2), generator=g, device=dev, dtype=torch.uint8)
+    s13 = (torch.rand((E, 2 * N, K // 32), generator=g, device=dev) * 0.015 + 0.02
+           ).to(torch.bfloat16)
+    s2 = (torch.rand((E, K, N // 32), generator=g, device=dev) * 0.015 + 0.02
+          ).to(torch.bfloat16)
+    w = (w13, w2, s13, s2)
+    torch.cuda.synchronize()
+    yield shape, w, tuple(t.cpu() for t in w)
+    del w
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dispatch", ["builtin", "table"])
+@pytest.mark.parametrize("M,skewed", [(64, True), (1024, False), (4096, False)])
+def test_reference_magnitudes_max_abs_full_size(pkg, orc, synth, dev, ref_magnitude_layer, M,
+                                                skewed, dispatch):
+    """max-abs <= 2e-2 in absolute terms (and rel-L2 <= 5e-3, and the tight
+    bounds) at the reference bench's magnitudes (x = randn/10,
+    bench/bench_moe.py:183-184, :243) at full size, on the paths of the
+    larger batches: skewed M=64 (the mixed GEMV + 64-slot MFMA launches),
+    M=1024 and M=4096 (192-slot MFMA tiles; the two-launch sort at 4096)."""
+    shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = ref_magnitude_layer
+    tuning = _dispatch(pkg, dispatch, M, shape, dev)
+    print(f"reference magnitudes M={M} skewed={skewed} ({dispatch}: {tuning})", flush=True)
+    x = synth.make_hidden(M, shape.K, dev, seed=M, scale=0.1)
+    tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=M, skewed=skewed)
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32, tuning=tuning)
+    torch.cuda.synchronize()
+    rl2, mab = _check(orc, out, x.cpu(), c13, c2, cs13, cs2, tw.cpu(), ti.cpu(), 32,
+                      f"reference magnitudes M={M} {dispatch}",
+                      bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K, tuning))
+    assert mab <= MAX_ABS_MAX, f"max-abs {mab} at M={M} {dispatch}"
+
+
+@pytest.mark.parametrize("M", [1024, 4096])
+def test_deterministic_full_size_prefill(pkg, synth, dev, full_layer, M):
+    """Run-to-run bit identity at full size on the prefill paths (192-slot
+    MFMA tiles, bf16 partial rows summed in slot order; the two-launch sort
+    at M=4096), with other calls dirtying the workspace in between."""
+    shape, (w13, w2, s13, s2), _ = full_layer
+    x = synth.make_hidden(M, shape.K, dev, seed=5)
+    tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=5)
+    print(f"determinism M={M}", flush=True)
+    a = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    for i in range(2):
+        x2 = synth.make_hidden(M, shape.K, dev, seed=60 + i)
+        tw2, ti2 = synth.make_routing(M, shape.E, shape.topk, dev, seed=60 + i, skewed=True)
+        pkg.fused_experts_w4a16(x2, w13, w2, s13, s2, tw2, ti2, 32)
+        b = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"M={M} run {i + 1}"
 
 
 @pytest.mark.parametrize("M,skewed", [(3, False), (8, True), (16, True)])

@@ -75,3 +75,63 @@ def test_noalloc_rejects_calls_beyond_the_scratch(pkg, lib):
     # M = 0 is a no-op that touches nothing
     assert lib.w4a16_moe_fused_experts_noalloc(P, 3072, P, P, P, P, P, P, 0, 10, 256, 1024,
                                                3072, 32, P, 3072, None, None) == L.W4A16_OK
+    # scales that are not 16-byte aligned (every expert then runs on the GEMV
+    # kernels, a layout of its own): the size check uses that layout and
+    # still answers with the scratch's own error, before any pointer check
+    for s13, s2 in ((P + 2, P), (P, P + 6)):
+        st = lib.w4a16_moe_fused_experts_noalloc(P, 3072, P, P, s13, s2, P, P, M, 10, 256,
+                                                 1024, 3072, 32, P, 3072, None, None)
+        assert st == L.W4A16_ERR_SCRATCH_TOO_SMALL, st
+    assert "device" in L.strerror(L.W4A16_ERR_WRONG_DEVICE)
+
+
+def test_noalloc_graph_replay(pkg, lib, synth, dev):
+    """One eager call (it resolves the scratch's address), then two calls of
+    different M captured into one HIP graph and replayed three times with
+    eager work between the replays; every replay's outputs equal the
+    workspace entry point's bit for bit."""
+    L = pkg._lib
+    shape = synth.LayerShape(E=32, topk=4, K=512, N=256, group=32)
+    w = synth.make_weights(shape, dev, seed=11)
+    Ms = (300, 7)
+    ins = []
+    for i, M in enumerate(Ms):
+        x = synth.make_hidden(M, shape.K, dev, seed=40 + i)
+        tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=40 + i, skewed=(i == 0))
+        ins.append((x, tw, ti))
+    expect = []
+    for (x, tw, ti), M in zip(ins, Ms):
+        b = torch.empty((M, shape.K), dtype=torch.bfloat16, device=dev)
+        nbytes = L.workspace_size(M, shape.topk, shape.E, shape.N, shape.K, shape.group)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        L.check(lib.w4a16_moe_fused_experts_ex(*_args(x, w, tw, ti, shape, b), ws.data_ptr(),
+                                                nbytes, torch.cuda.current_stream().cuda_stream,
+                                                None))
+        expect.append(b)
+    outs = [torch.empty((M, shape.K), dtype=torch.bfloat16, device=dev) for M in Ms]
+    # the eager call before capture resolves the scratch address on this device
+    x, tw, ti = ins[1]
+    L.check(lib.w4a16_moe_fused_experts_noalloc(*_args(x, w, tw, ti, shape, outs[1]),
+                                                torch.cuda.current_stream().cuda_stream, None))
+    torch.cuda.synchronize()
+    print("no-alloc graph: capture", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream().cuda_stream
+        for (x, tw, ti), o in zip(ins, outs):
+            L.check(lib.w4a16_moe_fused_experts_noalloc(*_args(x, w, tw, ti, shape, o), s, None))
+    for r in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        # eager work between replays: the scratch keeps this call's contents
+        x, tw, ti = ins[0]
+        junk = torch.empty_like(outs[0])
+        L.check(lib.w4a16_moe_fused_experts_noalloc(
+            *_args(synth.make_hidden(Ms[0], shape.K, dev, seed=90 + r), w, tw, ti, shape, junk),
+            torch.cuda.current_stream().cuda_stream, None))
+        torch.cuda.synchronize()
+        print(f"no-alloc graph: replay {r}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e, M in zip(outs, expect, Ms):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {r} M={M}"
