@@ -73,16 +73,6 @@ __device__ void block_exclusive_scan_n(const int (&v)[NV], int (&excl)[NV], int 
   __syncthreads();
 }
 
-// Exclusive scan of one int per thread over the workgroup; wave_tot is LDS
-// of 17 ints.  All threads must call.
-__device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
-  const int vv[1] = {v};
-  int ex[1], tt[1];
-  block_exclusive_scan_n<1>(vv, ex, tt, wave_tot);
-  *total = tt[0];
-  return ex[0];
-}
-
 // Token blocks (32 slots) of the tallest MFMA tile: the tile list is ordered
 // by height class, tallest first.
 constexpr int kTileClasses = kMfmaTileMMax / 32;
@@ -92,25 +82,40 @@ constexpr int kTileClasses = kMfmaTileMMax / 32;
 // 32 slots but the last); the tiles are listed by height class, tallest
 // first (experts ascending within a class), so that the MFMA launch starts
 // its longest tiles first.  Every other routed expert's single sorted block
-// goes to the GEMV list.  Thread tid owns experts e0 .. e0 + ipt - 1; wt is
-// LDS of (kTileClasses + 1) x 17 ints.  All threads must call.
-__device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const int32_t* off,
-                                 int e0, int ipt, int* wt) {
+// goes to the GEMV list.  Thread tid owns experts e0 .. e0 + ipt - 1.
+//
+// The lists take two parts around one workgroup scan, the one that also
+// gives the padded offsets (kScanSlots values per thread):
+//   scan_inputs   this thread's tiles per class (slots 0 .. NC - 1), GEMV
+//                 blocks (slot NC) and padded pair count (slot NC + 1);
+//   write_work_lists  the lists, from the scan's exclusive prefixes and
+//                 totals of slots 0 .. NC.
+constexpr int kScanSlots = kTileClasses + 2;
+
+// Tile height and count of an expert with c > gemv_max_tokens pairs.
+__device__ __forceinline__ void tile_split(int c, int tile_m, int& per, int& n_t) {
+  const int n_ch = (c + tile_m - 1) / tile_m;
+  per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
+  n_t = (c + per - 1) / per;
+}
+
+__device__ void scan_inputs(const AlignLaunch& a, const int32_t* tot, int e0, int ipt,
+                            int (&v)[kScanSlots]) {
   constexpr int NC = kTileClasses;
   const int E = a.num_experts, B = a.block, thr = a.gemv_max_tokens;
   // class of a tile of n slots: NC - (token blocks)
   auto cls = [](int n) { return NC - ((n + 31) >> 5); };
-  int v[NC + 1];  // tiles per class, then GEMV blocks
 #pragma unroll
-  for (int k = 0; k <= NC; ++k) v[k] = 0;
+  for (int k = 0; k < kScanSlots; ++k) v[k] = 0;
   for (int i = 0; i < ipt; ++i) {
     const int e = e0 + i;
     if (e >= E) break;
     const int c = tot[e];
+    v[NC + 1] += (c + B - 1) / B * B;
+    if (!a.tiles) continue;
     if (c > thr) {
-      const int n_ch = (c + a.tile_m - 1) / a.tile_m;
-      const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
-      const int n_t = (c + per - 1) / per;
+      int per, n_t;
+      tile_split(c, a.tile_m, per, n_t);
       const int kf = cls(per), kl = cls(c - (n_t - 1) * per);
 #pragma unroll
       for (int k = 0; k < NC; ++k) v[k] += (k == kf ? n_t - 1 : 0) + (k == kl ? 1 : 0);
@@ -118,21 +123,29 @@ __device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const
       ++v[NC];
     }
   }
-  int pos[NC + 1], total[NC + 1];
-  block_exclusive_scan_n<NC + 1>(v, pos, total, wt);
+}
+
+__device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const int32_t* off,
+                                 int e0, int ipt, const int (&excl)[kScanSlots],
+                                 const int (&total)[kScanSlots]) {
+  constexpr int NC = kTileClasses;
+  const int E = a.num_experts, B = a.block, thr = a.gemv_max_tokens;
+  auto cls = [](int n) { return NC - ((n + 31) >> 5); };
+  int pos[NC + 1];
   int n_tiles = 0;
 #pragma unroll
   for (int k = 0; k < NC; ++k) {
-    pos[k] += n_tiles;
+    pos[k] = excl[k] + n_tiles;
     n_tiles += total[k];
   }
+  pos[NC] = excl[NC];
   for (int i = 0; i < ipt; ++i) {
     const int e = e0 + i;
     if (e >= E) break;
     const int c = tot[e];
     if (c > thr) {
-      const int n_ch = (c + a.tile_m - 1) / a.tile_m;
-      const int per = ((c + n_ch - 1) / n_ch + 31) & ~31;
+      int per, n_t;
+      tile_split(c, a.tile_m, per, n_t);
       for (int s0 = 0; s0 < c; s0 += per) {
         const int n = min(per, c - s0);
         const int k = cls(n);
@@ -168,8 +181,7 @@ __device__ void write_expert_ids(const AlignLaunch& a, const int32_t* off, int t
 
 __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   extern __shared__ int32_t smem[];
-  __shared__ int32_t wave_tot[17];
-  __shared__ int32_t wl_tot[(kTileClasses + 1) * 17];
+  __shared__ int32_t scan_tot[kScanSlots * 17];
   __shared__ int32_t s_drop;
 
   const int nthr = blockDim.x;
@@ -253,16 +265,15 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   }
   __syncthreads();
 
-  // 3. offsets = exclusive scan of counts rounded up to the block size
+  // 3. offsets = exclusive scan of counts rounded up to the block size, in
+  // the same workgroup scan as the work lists' counts
   const int ipt = (E + nthr - 1) / nthr;
   const int e0 = tid * ipt;
-  int local = 0;
-  for (int i = 0; i < ipt; ++i) {
-    const int e = e0 + i;
-    if (e < E) local += (tot[e] + B - 1) / B * B;
-  }
-  int total = 0;
-  int excl = block_exclusive_scan(local, wave_tot, &total);
+  int sv[kScanSlots], sx[kScanSlots], st[kScanSlots];
+  scan_inputs(a, tot, e0, ipt, sv);
+  block_exclusive_scan_n<kScanSlots>(sv, sx, st, scan_tot);
+  const int total = st[kScanSlots - 1];
+  int excl = sx[kScanSlots - 1];
   for (int i = 0; i < ipt; ++i) {
     const int e = e0 + i;
     if (e < E) {
@@ -274,7 +285,7 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   __syncthreads();
 
   // 3b. work lists of the fused call
-  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, wl_tot);
+  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, sx, st);
 
   for (int i = tid; i < nw * E; i += nthr) cnt[i] += off[i % E];
   __syncthreads();
@@ -376,8 +387,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
                                                              const int32_t* ctot,
                                                              const int32_t* cdrop) {
   extern __shared__ int32_t smem[];
-  __shared__ int32_t wave_tot[17];
-  __shared__ int32_t wl_tot[(kTileClasses + 1) * 17];
+  __shared__ int32_t scan_tot[kScanSlots * 17];
   constexpr int nw = kChunkWaves;
   const int tid = threadIdx.x;
   const int wid = tid >> 6;
@@ -433,16 +443,15 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   }
   __syncthreads();
 
-  // 4. offsets = exclusive scan of the padded totals
+  // 4. offsets = exclusive scan of the padded totals, in the same workgroup
+  // scan as the work lists' counts (which workgroup 0 writes)
   const int ipt = (E + kChunk - 1) / kChunk;
   const int e0 = tid * ipt;
-  int local = 0;
-  for (int i = 0; i < ipt; ++i) {
-    const int e = e0 + i;
-    if (e < E) local += (tot[e] + B - 1) / B * B;
-  }
-  int total = 0;
-  int excl = block_exclusive_scan(local, wave_tot, &total);
+  int sv[kScanSlots], sx[kScanSlots], st[kScanSlots];
+  scan_inputs(a, tot, e0, ipt, sv);
+  block_exclusive_scan_n<kScanSlots>(sv, sx, st, scan_tot);
+  const int total = st[kScanSlots - 1];
+  int excl = sx[kScanSlots - 1];
   for (int i = 0; i < ipt; ++i) {
     const int e = e0 + i;
     if (e < E) {
@@ -467,7 +476,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   if (g != 0) return;
 
   // 6. workgroup 0: work lists, sentinels, block experts, scalars
-  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, wl_tot);
+  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, sx, st);
   for (int e = tid; e < E; e += kChunk) {
     const int p1 = off[e + 1];
     for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
