@@ -604,6 +604,20 @@ def stage_roofline(wl, stage, us):
             "algorithmic_flops_per_launch": int(flops)}
 
 
+def trace_from_profile(kernel, config_index):
+    """The rocprofv3 kernel-trace average duration (us) recorded in profiles/
+    for this kernel/config: every launch of a profiled bench run, cold graph
+    launches included."""
+    import re
+
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            m = re.match(r"\s*trace_avg_us\[(\w+), config (\d+)\]:\s*([0-9.]+)", line)
+            if m and m.group(1) == kernel and int(m.group(2)) == config_index:
+                return float(m.group(3)), str(path.relative_to(ROOT))
+    return None, None
+
+
 def traffic_from_profile(kernel, config_index):
     """The HBM bytes per launch recorded in profiles/ for this kernel/config."""
     import re
@@ -696,7 +710,17 @@ def main(argv=None) -> int:
     else:
         traffic, traffic_src = traffic_from_profile(dominant, head_cfg.index)
     roofline.update({"traffic": traffic, "traffic_source": traffic_src,
-                     "avg_launch_us": round(stages[dominant] * 1e3, 3)})
+                     "avg_launch_us": round(stages[dominant] * 1e3, 3),
+                     "timing": "stage graph: p50 replay of graphs of the dominant kernel "
+                               "alone over the rotating sets / launches, HIP events on "
+                               "the launch stream"})
+    # The same roofline at the committed kernel trace's average duration (it
+    # includes the first, cold launch of each graph), for comparison.
+    trace_us, trace_src = trace_from_profile(dominant, head_cfg.index)
+    if trace_us:
+        rt = stage_roofline(wl, dominant, trace_us)
+        roofline["trace"] = {"avg_launch_us": trace_us, "achieved": rt["achieved"],
+                             "frac": rt["frac"], "source": trace_src}
 
     sweep = []
     if not args.no_sweep:
