@@ -259,6 +259,13 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
   u32x4_t* xp = lds;
   float* xc = reinterpret_cast<float*>(lds + TC * row_oct);
 
+  // The one-token launches (one row per pass, 32 lanes per weight row: every
+  // workgroup starts at once and each waits on the routing, then on its
+  // first weights) raise the issue priority until the staged rows are in
+  // place: M=1 16.20 -> 15.97 us per call.  The same made M=2 (two rows per
+  // pass) and M=16 (8-lane rows) slower: 26.37 -> 26.84, 122.6 -> 123.9 us.
+  constexpr bool kProloguePrio = LPR == 32 && TC == 1;
+  if constexpr (kProloguePrio) __builtin_amdgcn_s_setprio(1);
   int e, T, f_lane = 0;
   int fl[4];
   if constexpr (ROUTE) {
@@ -507,6 +514,7 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
         }
       }
       __syncthreads();
+      if constexpr (kProloguePrio) __builtin_amdgcn_s_setprio(0);
 
       float acc[NR][NTOK];
       auto clear = [&]() {
