@@ -18,7 +18,8 @@
 //   5. padding slots and the tail get the sentinel M*topk, each expert's
 //      thread writes the expert id of the blocks it owns (what searchsorted
 //      right=True of the block starts over the offsets gives), blocks past
-//      the padded end get -1.
+//      the padded end get -1 -- written as soon as the offsets are known,
+//      before step 4, so that these stores drain during the placement.
 // Integer only; the output is bit-identical to the reference over the whole
 // fixed-size buffers.  Ids outside [0, E) are skipped and counted.
 #include "common.hpp"
@@ -26,51 +27,77 @@
 namespace w4a16 {
 namespace {
 
-// Inclusive scan over the 64 lanes of a wave with DPP lane moves (no LDS):
-// shifts by 1, 2, 4 and 8 lanes inside each row of 16 (lanes without a source
-// add 0), then the last lane of row 0 is added to row 1 and of row 2 to row 3
-// (row_bcast:15), then the last lane of row 1 to rows 2 and 3 (row_bcast:31).
-__device__ __forceinline__ int wave_inclusive_scan(int x) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
-  return x;
+// Workgroup barrier for LDS only: the kernels here share data through LDS
+// alone (no thread reads another's global stores), so a barrier waits for
+// the wave's LDS accesses and leaves its global loads and stores in flight
+// -- a __syncthreads() fence would wait for every one of them (the ids'
+// loads while the counts are cleared, the sentinel stores during the
+// placement).  The memory clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// NV exclusive scans of one int per thread over the workgroup at once (three
-// barriers); wt is LDS of NV x 17 ints.  All threads must call.
+// NV inclusive scans over the 64 lanes of a wave with DPP lane moves (no
+// LDS), step by step over all NV values so that the independent moves fill
+// each other's wait states: shifts by 1, 2, 4 and 8 lanes inside each row of
+// 16 (lanes without a source add 0), then the last lane of row 0 is added to
+// row 1 and of row 2 to row 3 (row_bcast:15), then the last lane of row 1 to
+// rows 2 and 3 (row_bcast:31).
+template <int NV>
+__device__ __forceinline__ void wave_inclusive_scan_n(int (&x)[NV]) {
+#define W4A16_SCAN_STEP(CTRL, ROWS, BC)                                        \
+  _Pragma("unroll") for (int k = 0; k < NV; ++k)                               \
+    x[k] += __builtin_amdgcn_update_dpp(0, x[k], CTRL, ROWS, 0xF, BC);
+  W4A16_SCAN_STEP(0x111, 0xF, true)   // row_shr:1
+  W4A16_SCAN_STEP(0x112, 0xF, true)   // row_shr:2
+  W4A16_SCAN_STEP(0x114, 0xF, true)   // row_shr:4
+  W4A16_SCAN_STEP(0x118, 0xF, true)   // row_shr:8
+  W4A16_SCAN_STEP(0x142, 0xA, false)  // row_bcast:15
+  W4A16_SCAN_STEP(0x143, 0xC, false)  // row_bcast:31
+#undef W4A16_SCAN_STEP
+}
+
+// NV exclusive scans of one int per thread over the workgroup at once, for
+// values that are zero outside waves w0 .. w0 + nv - 1: those waves scan
+// their own values, and after one barrier every thread sums the wave totals
+// it needs from LDS.  wt is 16-byte aligned LDS of 16 NV ints, not reused
+// before the caller's next barrier.  All threads must call.
 template <int NV>
 __device__ void block_exclusive_scan_n(const int (&v)[NV], int (&excl)[NV], int (&total)[NV],
-                                       int* wt) {
+                                       int* wt, int w0, int nv) {
+  static_assert(NV % 4 == 0, "wave totals are read 4 at a time");
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
-  const int nw = blockDim.x >> 6;
+  const int wr = wid - w0;  // the wave's rank among the scanning waves
   int x[NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    x[k] = wave_inclusive_scan(v[k]);
-    if (lane == 63) wt[k * 17 + wid] = x[k];
-  }
-  __syncthreads();
-  if (wid == 0) {
+  for (int k = 0; k < NV; ++k) x[k] = v[k];
+  if (wr >= 0 && wr < nv) {
+    wave_inclusive_scan_n<NV>(x);
+    if (lane == 63) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int t = lane < nw ? wt[k * 17 + lane] : 0;
-      const int sc = wave_inclusive_scan(t);
-      if (lane < nw) wt[k * 17 + lane] = sc - t;
-      if (lane == nw - 1) wt[k * 17 + 16] = sc;
+      for (int k = 0; k < NV; ++k) wt[wr * NV + k] = x[k];
     }
   }
-  __syncthreads();
+  lds_barrier();
+  int pre[NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    total[k] = wt[k * 17 + 16];
-    excl[k] = x[k] - v[k] + wt[k * 17 + wid];
+  for (int k = 0; k < NV; ++k) pre[k] = total[k] = 0;
+  for (int w = 0; w < nv; ++w) {
+#pragma unroll
+    for (int k4 = 0; k4 < NV; k4 += 4) {
+      const int4 t = *reinterpret_cast<const int4*>(wt + w * NV + k4);
+      const int tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        total[k4 + k] += tv[k];
+        pre[k4 + k] += w < wr ? tv[k] : 0;
+      }
+    }
   }
-  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NV; ++k) excl[k] = wr < 0 ? 0 : wr < nv ? x[k] - v[k] + pre[k] : total[k];
 }
 
 // Token blocks (32 slots) of the tallest MFMA tile: the tile list is ordered
@@ -92,11 +119,27 @@ constexpr int kTileClasses = kMfmaTileMMax / 32;
 //                 totals of slots 0 .. NC.
 constexpr int kScanSlots = kTileClasses + 2;
 
+// n / d for n >= 0, d >= 1: below 2^22 a float quotient (the hardware
+// reciprocal, off from n / d by less than 1) corrected by one step each way
+// -- exact, in a few instructions instead of an integer division's ~35.
+__device__ __forceinline__ int div_small(int n, int d) {
+  if (n >= (1 << 22) || d >= (1 << 22)) return n / d;
+  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
+  q -= q * d > n ? 1 : 0;
+  q += (q + 1) * d <= n ? 1 : 0;
+  return q;
+}
+
 // Tile height and count of an expert with c > gemv_max_tokens pairs.
 __device__ __forceinline__ void tile_split(int c, int tile_m, int& per, int& n_t) {
-  const int n_ch = (c + tile_m - 1) / tile_m;
-  per = ((c + n_ch - 1) / n_ch + 31) & ~31;  // <= tile_m
-  n_t = (c + per - 1) / per;
+  const int n_ch = div_small(c + tile_m - 1, tile_m);
+  per = (div_small(c + n_ch - 1, n_ch) + 31) & ~31;  // <= tile_m
+  n_t = div_small(c + per - 1, per);
+}
+
+// c rounded up to a multiple of the block size B.
+__device__ __forceinline__ int round_up_block(int c, int B) {
+  return div_small(c + B - 1, B) * B;
 }
 
 __device__ void scan_inputs(const AlignLaunch& a, const int32_t* tot, int e0, int ipt,
@@ -111,7 +154,7 @@ __device__ void scan_inputs(const AlignLaunch& a, const int32_t* tot, int e0, in
     const int e = e0 + i;
     if (e >= E) break;
     const int c = tot[e];
-    v[NC + 1] += (c + B - 1) / B * B;
+    v[NC + 1] += round_up_block(c, B);
     if (!a.tiles) continue;
     if (c > thr) {
       int per, n_t;
@@ -127,7 +170,7 @@ __device__ void scan_inputs(const AlignLaunch& a, const int32_t* tot, int e0, in
 
 __device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const int32_t* off,
                                  int e0, int ipt, const int (&excl)[kScanSlots],
-                                 const int (&total)[kScanSlots]) {
+                                 const int (&total)[kScanSlots], bool scalars) {
   constexpr int NC = kTileClasses;
   const int E = a.num_experts, B = a.block, thr = a.gemv_max_tokens;
   auto cls = [](int n) { return NC - ((n + 31) >> 5); };
@@ -156,32 +199,60 @@ __device__ void write_work_lists(const AlignLaunch& a, const int32_t* tot, const
         a.tiles[p] = make_int4(e, off[e] + s0, n, 0);
       }
     } else if (c > 0) {
-      a.gemv_blocks[pos[NC]++] = off[e] / B;
+      a.gemv_blocks[pos[NC]++] = div_small(off[e], B);
     }
   }
-  if (threadIdx.x == 0) {
+  if (scalars) {
     a.n_tiles[0] = n_tiles;
     a.n_gemv[0] = total[NC];
   }
 }
 
-// Block b's expert (-1 past the padded total): expert e owns blocks
-// off[e] / B .. off[e+1] / B - 1 (the offsets are multiples of B), so each
-// expert's thread writes its own -- the searchsorted(right) of the
-// reference's block starts over the offsets, without a search per block.
-__device__ void write_expert_ids(const AlignLaunch& a, const int32_t* off, int total, int tid,
-                                 int nthr) {
-  const int B = a.block;
-  for (int e = tid; e < a.num_experts; e += nthr) {
-    const int b1 = min(off[e + 1] / B, a.n_blocks);
-    for (int b = off[e] / B; b < b1; ++b) a.expert_ids[b] = e;
+// The padding of the sorted ids and of the block experts, by threads t of nt
+// (the whole workgroup), once the counts and offsets are known:
+//   * expert e's padding slots off[e] + tot[e] .. off[e+1] - 1 get the
+//     sentinel from tpe = max(1, nt / E) threads, every tpe-th slot each;
+//   * the tail slots from the padded total on get it too, 16 bytes per store
+//     where the buffer is 16-byte aligned;
+//   * blocks from the padded total on get expert -1.
+__device__ void write_padding(const AlignLaunch& a, const int32_t* tot, const int32_t* off,
+                              int total, int t, int nt) {
+  const int E = a.num_experts, B = a.block, sent = a.n_tok, em = a.em;
+  int32_t* const sorted = a.sorted;
+  const int tpe = max(1, div_small(nt, E));
+  for (int idx = t; idx < E * tpe; idx += nt) {
+    const int e = div_small(idx, tpe);
+    for (int p = off[e] + tot[e] + (idx - e * tpe); p < off[e + 1]; p += tpe) sorted[p] = sent;
   }
-  for (int b = total / B + tid; b < a.n_blocks; b += nthr) a.expert_ids[b] = -1;
+  int p4 = em;  // start of the 16-byte stores (none when unaligned)
+  if ((reinterpret_cast<uintptr_t>(sorted) & 15) == 0) {
+    p4 = min(em, (total + 3) & ~3);
+    const int n4 = (em - p4) >> 2;
+    const int4 s4 = make_int4(sent, sent, sent, sent);
+    for (int i = t; i < n4; i += nt) reinterpret_cast<int4*>(sorted + p4)[i] = s4;
+    for (int p = p4 + 4 * n4 + t; p < em; p += nt) sorted[p] = sent;
+  }
+  for (int p = total + t; p < p4; p += nt) sorted[p] = sent;
+  for (int b = div_small(total, B) + t; b < a.n_blocks; b += nt) a.expert_ids[b] = -1;
+}
+
+// Block b's expert for the blocks of experts e0 .. e0 + ipt - 1: expert e
+// owns blocks off[e] / B .. off[e+1] / B - 1 (the offsets are multiples of
+// B), so each expert's thread writes its own -- the searchsorted(right) of
+// the reference's block starts over the offsets, without a search per block.
+__device__ void write_block_experts(const AlignLaunch& a, const int32_t* off, int e0, int ipt) {
+  const int B = a.block, E = a.num_experts;
+  for (int i = 0; i < ipt; ++i) {
+    const int e = e0 + i;
+    if (e >= E) break;
+    const int b1 = min(div_small(off[e + 1], B), a.n_blocks);
+    for (int b = div_small(off[e], B); b < b1; ++b) a.expert_ids[b] = e;
+  }
 }
 
 __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   extern __shared__ int32_t smem[];
-  __shared__ int32_t scan_tot[kScanSlots * 17];
+  __shared__ __align__(16) int32_t scan_tot[kScanSlots * 16];
   __shared__ int32_t s_drop;
 
   const int nthr = blockDim.x;
@@ -197,10 +268,6 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   int32_t* off = cnt + nw * E;   // [E+1]
   int32_t* tot = off + E + 1;    // [E]
 
-  for (int i = tid; i < nw * E; i += nthr) cnt[i] = 0;
-  if (tid == 0) s_drop = 0;
-  __syncthreads();
-
   // Contiguous chunk of flat indices per wave, a multiple of 64.
   const int per = ((n_tok + nw - 1) / nw + 63) & ~63;
   const int beg = min(n_tok, wid * per);
@@ -209,12 +276,14 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   // Ids are read kBatch * 64 at a time per wave, every load issued before
   // the first is used: one memory latency per batch, not per 64 ids.
   constexpr int kBatch = 8;
+  // Lanes past the wave's end load a clamped (in-bounds) entry; both walks
+  // below test f < end before using a value, so nothing here waits for the
+  // loads.
   auto load_batch = [&](int f0, int (&ev)[kBatch]) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int f = f0 + 64 * u + lane;
-      const int v = a.ids[min(f, max(end - 1, 0))];  // clamped, in bounds
-      ev[u] = f < end ? v : -1;
+      ev[u] = a.ids[min(f, max(end - 1, 0))];
     }
   };
 
@@ -226,6 +295,11 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
   const bool one_batch = end - beg <= 64 * kBatch;  // uniform
   int ev1[kBatch];
   if (one_batch && beg < end) load_batch(beg, ev1);
+
+  // (the ids' loads are in flight while the counts are cleared)
+  for (int i = tid; i < nw * E; i += nthr) cnt[i] = 0;
+  if (tid == 0) s_drop = 0;
+  lds_barrier();
 
   // 1. per-wave histogram
   int drop = 0;
@@ -251,7 +325,7 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
     }
   }
   if (drop) atomicAdd(&s_drop, drop);
-  __syncthreads();
+  lds_barrier();
 
   // 2. column prefix over waves: cnt[w][e] <- rank of wave w's first pair
   for (int e = tid; e < E; e += nthr) {
@@ -263,34 +337,53 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
     }
     tot[e] = run;
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. offsets = exclusive scan of counts rounded up to the block size, in
-  // the same workgroup scan as the work lists' counts
+  // the same workgroup scan as the work lists' counts.  The experts belong to
+  // n_own threads (ipt each, ascending): the workgroup's last ones when their
+  // waves hold no ids, so that the expert-parallel writes after the scan
+  // overlap the placement, else its first ones.
   const int ipt = (E + nthr - 1) / nthr;
-  const int e0 = tid * ipt;
+  const int n_own = (E + ipt - 1) / ipt;
+  const int own_waves = (n_own + 63) >> 6;
+  const bool own_last = (n_tok + per - 1) / per <= nw - own_waves;
+  const int own0 = own_last ? nthr - n_own : 0;  // first owner thread
+  const int own = tid - own0;                    // in [0, n_own): an owner
+  const int e0 = own >= 0 && own < n_own ? own * ipt : E;
   int sv[kScanSlots], sx[kScanSlots], st[kScanSlots];
   scan_inputs(a, tot, e0, ipt, sv);
-  block_exclusive_scan_n<kScanSlots>(sv, sx, st, scan_tot);
+  block_exclusive_scan_n<kScanSlots>(sv, sx, st, scan_tot, own0 >> 6,
+                                     own_last ? nw - (own0 >> 6) : own_waves);
   const int total = st[kScanSlots - 1];
   int excl = sx[kScanSlots - 1];
   for (int i = 0; i < ipt; ++i) {
     const int e = e0 + i;
     if (e < E) {
       off[e] = excl;
-      excl += (tot[e] + B - 1) / B * B;
+      excl += round_up_block(tot[e], B);
     }
   }
-  if (tid == 0) off[E] = total;
-  __syncthreads();
+  if (own == 0) off[E] = total;
+  lds_barrier();
 
-  // 3b. work lists of the fused call
-  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, sx, st);
+  // 3b. the outputs that need only the counts and offsets: the owners' work
+  // lists of the fused call, block experts and scalars, everyone's share of
+  // the padding -- while the placement writes the other sorted positions
+  if (own >= 0 && own < n_own) {
+    if (a.tiles) write_work_lists(a, tot, off, e0, ipt, sx, st, own == 0);
+    write_block_experts(a, off, e0, ipt);
+    if (a.offsets)
+      for (int e = own; e <= E; e += n_own) a.offsets[e] = off[e];
+    if (own == 0) {
+      a.num_post[0] = total;
+      if (a.dropped) a.dropped[0] = s_drop;
+    }
+  }
+  write_padding(a, tot, off, total, tid, nthr);
 
-  for (int i = tid; i < nw * E; i += nthr) cnt[i] += off[i % E];
-  __syncthreads();
-
-  // 4. stable placement
+  // 4. stable placement: the pair's slot is its expert's offset plus its rank
+  // (cnt holds each wave's next rank inside every expert)
   int ebits = 0;
   while ((1 << ebits) < E) ++ebits;
   const uint64_t lt = lanemask_lt();
@@ -315,31 +408,18 @@ __global__ __launch_bounds__(1024) void align_kernel(const AlignLaunch a) {
         const uint64_t m = ballot(set);
         peers &= set ? m : ~m;
       }
-      int base = 0;
-      if (ok) base = cnt[wid * E + e];
+      int base = 0, eoff = 0;
+      if (ok) base = cnt[wid * E + e], eoff = off[e];
       __builtin_amdgcn_wave_barrier();
       if (ok) {
         const uint64_t below = peers & lt;
-        a.sorted[base + __popcll(below)] = f;
+        a.sorted[eoff + base + __popcll(below)] = f;
         if (below == 0) cnt[wid * E + e] = base + __popcll(peers);
       }
       __builtin_amdgcn_wave_barrier();
     }
   }
 
-  // 5. sentinels, expert ids, scalars
-  for (int e = tid; e < E; e += nthr) {
-    const int p1 = off[e + 1];
-    for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
-  }
-  for (int p = total + tid; p < a.em; p += nthr) a.sorted[p] = n_tok;
-  write_expert_ids(a, off, total, tid, nthr);
-  if (a.offsets)
-    for (int e = tid; e <= E; e += nthr) a.offsets[e] = off[e];
-  if (tid == 0) {
-    a.num_post[0] = total;
-    if (a.dropped) a.dropped[0] = s_drop;
-  }
 }
 
 // ---- many workgroups (large batches) --------------------------------------
@@ -364,7 +444,7 @@ __global__ __launch_bounds__(kChunk) void align_count_kernel(const AlignLaunch a
   const int E = a.num_experts;
   const int tid = threadIdx.x;
   for (int i = tid; i <= E; i += kChunk) hist[i] = 0;
-  __syncthreads();
+  lds_barrier();
   const int f = blockIdx.x * kChunk + tid;
   int drop = 0;
   if (f < a.n_tok) {
@@ -376,9 +456,9 @@ __global__ __launch_bounds__(kChunk) void align_count_kernel(const AlignLaunch a
   }
   // dropped pairs of the chunk: one wave-level ballot count per wave
   const int wd = __popcll(ballot(drop != 0));
-  __syncthreads();
+  lds_barrier();
   if ((tid & 63) == 0 && wd) atomicAdd(&hist[E], wd);
-  __syncthreads();
+  lds_barrier();
   for (int i = tid; i < E; i += kChunk) ctot[(int64_t)blockIdx.x * E + i] = hist[i];
   if (tid == 0) cdrop[blockIdx.x] = hist[E];
 }
@@ -387,7 +467,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
                                                              const int32_t* ctot,
                                                              const int32_t* cdrop) {
   extern __shared__ int32_t smem[];
-  __shared__ int32_t scan_tot[kScanSlots * 17];
+  __shared__ __align__(16) int32_t scan_tot[kScanSlots * 16];
   constexpr int nw = kChunkWaves;
   const int tid = threadIdx.x;
   const int wid = tid >> 6;
@@ -406,7 +486,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   // (independent loads in flight), combined with LDS atomics
   for (int i = tid; i < nw * E; i += kChunk) cnt[i] = 0;
   for (int e = tid; e < E; e += kChunk) tot[e] = off[e] = 0;
-  __syncthreads();
+  lds_barrier();
   {
     const int parts = max(1, kChunk / E);
     const int part = tid / E;
@@ -423,14 +503,14 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
       atomicAdd(&off[e], before);  // parked here until the offsets are known
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 2. this chunk's per-wave histograms (wave w: pairs 64 w .. of the chunk)
   const int f = g * kChunk + tid;
   const int e_me = f < n_tok ? a.ids[f] : -1;
   const bool ok = f < n_tok && e_me >= 0 && e_me < E;
   if (ok) atomicAdd(&cnt[wid * E + e_me], 1);
-  __syncthreads();
+  lds_barrier();
 
   // 3. column prefix over the waves, on top of the chunk's starting rank
   for (int e = tid; e < E; e += kChunk) {
@@ -441,7 +521,7 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
       run += c;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 4. offsets = exclusive scan of the padded totals, in the same workgroup
   // scan as the work lists' counts (which workgroup 0 writes)
@@ -449,18 +529,19 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   const int e0 = tid * ipt;
   int sv[kScanSlots], sx[kScanSlots], st[kScanSlots];
   scan_inputs(a, tot, e0, ipt, sv);
-  block_exclusive_scan_n<kScanSlots>(sv, sx, st, scan_tot);
+  // the owners (e0 < E) are threads 0 .. ceil(E / ipt) - 1
+  block_exclusive_scan_n<kScanSlots>(sv, sx, st, scan_tot, 0, ((E + ipt - 1) / ipt + 63) >> 6);
   const int total = st[kScanSlots - 1];
   int excl = sx[kScanSlots - 1];
   for (int i = 0; i < ipt; ++i) {
     const int e = e0 + i;
     if (e < E) {
       off[e] = excl;
-      excl += (tot[e] + B - 1) / B * B;
+      excl += round_up_block(tot[e], B);
     }
   }
   if (tid == 0) off[E] = total;
-  __syncthreads();
+  lds_barrier();
 
   // 5. stable placement: lanes routed to the same expert find each other
   // with ballots over the expert-id bits and take their rank among them
@@ -476,13 +557,9 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
   if (g != 0) return;
 
   // 6. workgroup 0: work lists, sentinels, block experts, scalars
-  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, sx, st);
-  for (int e = tid; e < E; e += kChunk) {
-    const int p1 = off[e + 1];
-    for (int p = off[e] + tot[e]; p < p1; ++p) a.sorted[p] = n_tok;
-  }
-  for (int p = total + tid; p < a.em; p += kChunk) a.sorted[p] = n_tok;
-  write_expert_ids(a, off, total, tid, kChunk);
+  if (a.tiles) write_work_lists(a, tot, off, e0, ipt, sx, st, tid == 0);
+  write_block_experts(a, off, e0, ipt);
+  write_padding(a, tot, off, total, tid, kChunk);
   if (a.offsets)
     for (int e = tid; e <= E; e += kChunk) a.offsets[e] = off[e];
   if (tid == 0) {
