@@ -197,7 +197,8 @@ hipError_t launch_gemv_n(const GemvLaunch& a, hipStream_t stream) {
   const int chunks = a.n_out / rows_per_wave;
   const int slabs = (chunks + W - 1) / W;
   const int groups = (slabs + UPW - 1) / UPW;
-  const size_t lds = gemv_lds_bytes(TC, a.kdim);
+  const size_t lds =
+      ROUTE ? gemv_route_lds_bytes(TC, a.kdim, a.num_experts) : gemv_lds_bytes(TC, a.kdim);
   if (lds > kMaxLds) return hipErrorInvalidValue;
   if (ROUTE && (a.n_tok < 1 || a.n_tok > kRouteMaxTok)) return hipErrorInvalidValue;
   const int64_t grid = (int64_t)(ROUTE ? a.max_items : a.max_blocks) * groups;
@@ -290,9 +291,9 @@ hipError_t launch_w13_gemv(const GemvLaunch& a_in, hipStream_t stream) {
 }
 
 bool gemv_route_fits(int n_tok, int num_experts, int K, int N) {
-  (void)num_experts;
-  return n_tok >= 1 && n_tok <= kRouteMaxTok && gemv_lds_bytes(1, K) <= kMaxLds &&
-         gemv_lds_bytes(1, N) <= kMaxLds;
+  return n_tok >= 1 && n_tok <= kRouteMaxTok &&
+         gemv_route_lds_bytes(1, K, num_experts) <= kMaxLds &&
+         gemv_route_lds_bytes(1, N, num_experts) <= kMaxLds;
 }
 
 bool w2_token_fits(int topk, int K, int N) {

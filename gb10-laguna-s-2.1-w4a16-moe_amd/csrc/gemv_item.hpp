@@ -143,19 +143,31 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
   return pos;
 }
 
-// Self-routing in registers, by every wave on its own (no LDS, no barrier).
-// Work item `item` is flat slot `item`; it carries work only when that slot
-// is the first (lowest flat index) routed to its expert, and then covers all
-// of the expert's pairs in ascending flat index -- the order
+// Self-routing, by every wave on its own (no barrier).  A work item covers
+// all of one expert's pairs in ascending flat index -- the order
 // moe_align_block_size gives them (kernels/w4a16_moe.py:243-278).  Lane l
 // gets in fl[j] the flat index of the expert's pair of rank l + 64 j (n_tok
-// past the last).  e_out = -1 when the item has no work; dropped = pairs with
-// ids outside [0, E).  Requires 1 <= n_tok <= kRouteMaxTok.
+// past the last).  e_out = -1 when the item has no work; dropped = pairs
+// with ids outside [0, E).  Requires 1 <= n_tok <= kRouteMaxTok.
+// By default work item `item` is flat slot `item`, with work when that slot
+// is the first routed to its expert (one ballot).  COMPACT (the w13 launch)
+// from 65 pairs, where many slots repeat an earlier slot's expert: work item
+// `item` is the item-th first slot in flat order, so the items with work fill
+// the start of the grid and the empty ones (past the number of routed
+// experts) its end, where they hold a slot in the launch's tail rather than
+// among the streaming workgroups: M=16 123.0 -> 121.8 us per call, M=12
+// 102.8 -> 102.2, skewed M=8, 12, 16 57.2 -> 56.1, 72.4 -> 70.8, 93.2 ->
+// 91.8.  The same search on the shorter w2 workgroups cost more than it
+// saved (uniform M=8, 12, 16: +1.0, +1.5, +0.2 us), and below 65 pairs on
+// both (M=2 25.9 -> 26.6).  tab: this wave's
+// E ints of LDS, where the first slot of every expert is a minimum over the
+// slots (a wave's LDS instructions run in order, so no wait separates the
+// steps).
 // NQ: ids per lane actually read (1 when n_tok <= 64, else 4); the lanes'
 // further ids count as absent.
-template <int NQ>
+template <int NQ, bool COMPACT>
 __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e_out,
-                                           int& t_out, int (&fl)[4], int& dropped) {
+                                           int& t_out, int (&fl)[4], int& dropped, int* tab) {
   const int lane = __lane_id();
   const int n_tok = a.n_tok, E = a.num_experts;
   constexpr int kNone = -2147483647 - 1;
@@ -176,12 +188,44 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
   for (int j = 0; j < 4; ++j) fl[j] = n_tok;
   e_out = -1;
   t_out = 0;
-  const int e = __builtin_amdgcn_readfirstlane(a.ids[item]);
-  if (e < 0 || e >= E) return;
-  bool earlier = false;
+  int e;
+  if (!COMPACT || NQ == 1 || n_tok <= a.topk) {
+    e = __builtin_amdgcn_readfirstlane(a.ids[item]);
+    if (e < 0 || e >= E) return;
+    bool earlier = false;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) earlier |= (lane + 64 * q < item) && id[q] == e;
-  if (ballot(earlier) != 0) return;  // an earlier slot's item owns this expert
+    for (int q = 0; q < NQ; ++q) earlier |= (lane + 64 * q < item) && id[q] == e;
+    if (ballot(earlier) != 0) return;  // an earlier slot's item owns this expert
+  } else {
+    auto valid = [&](int v) { return v >= 0 && v < E; };
+    for (int x = lane; x < E; x += 64) tab[x] = n_tok;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      if (valid(id[q])) atomicMin(&tab[id[q]], lane + 64 * q);
+    asm volatile("" ::: "memory");
+    uint64_t F[4];
+    int cF[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      F[q] = q < NQ ? ballot(valid(id[q]) && tab[id[q]] == lane + 64 * q) : 0ull;
+      cF[q] = __popcll(F[q]);
+    }
+    // the item-th first-occurrence slot, and its expert
+    int p = 0, qs = -1, ks = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (qs < 0 && item < p + cF[q]) qs = q, ks = item - p;
+      p += cF[q];
+    }
+    if (qs < 0) return;  // past the routed experts (uniform)
+    uint64_t Fs = F[0];
+    int vs = id[0];
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (qs == q) Fs = F[q], vs = id[q];
+    e = __builtin_amdgcn_readfirstlane(__shfl(vs, nth_set_bit(Fs, ks), 64));
+  }
   uint64_t m[4];
   int c[4];
   int T = 0;
@@ -270,10 +314,12 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
   int fl[4];
   if constexpr (ROUTE) {
     int dropped;
+    // this wave's routing table, past the staged rows (gemv_route_lds_bytes)
+    int* tab = reinterpret_cast<int*>(xc + TC * xc_pitch) + wid * a.num_experts;
     if (a.n_tok <= 64)
-      route_wave<1>(a, item, e, T, fl, dropped);
+      route_wave<1, MODE == 0>(a, item, e, T, fl, dropped, tab);
     else
-      route_wave<4>(a, item, e, T, fl, dropped);
+      route_wave<4, MODE == 0>(a, item, e, T, fl, dropped, tab);
     if (MODE == 0 && bid == 0 && tid == 0) a.dropped_out[0] = dropped;
     if (e < 0) return;  // workgroup-uniform: every wave routes the same item
   } else {
@@ -619,6 +665,12 @@ size_t gemv_lds_bytes(int tc, int kdim) {
   return tc * (row_oct * sizeof(u32x4_t) + (size_t)((kdim >> 5) + 1) * sizeof(float));
 }
 
+// LDS of a self-routing launch: the staged rows, then each wave's routing
+// table (one int per expert).
+size_t gemv_route_lds_bytes(int tc, int kdim, int num_experts) {
+  return gemv_lds_bytes(tc, kdim) + (size_t)kGemvWaves * (size_t)num_experts * sizeof(int);
+}
+
 // Launch shapes: output rows per lane (RPL) and prefetch depth (PF) of the
 // two GEMVs, waves per workgroup.  w2's passes of four token rows have their
 // own shape (_T4): 4 rows per lane with 2 steps in flight moves the same
@@ -666,7 +718,10 @@ int pick_tc(const GemvLaunch& a, int num_experts) {
     tc = 1;
   else if (M < 8)
     tc = 2;
-  while (tc > 1 && gemv_lds_bytes(tc, a.kdim) > kMaxLds) tc >>= 1;
+  auto lds = [&](int t) {
+    return a.ids ? gemv_route_lds_bytes(t, a.kdim, num_experts) : gemv_lds_bytes(t, a.kdim);
+  };
+  while (tc > 1 && lds(tc) > kMaxLds) tc >>= 1;
   return tc;
 }
 
