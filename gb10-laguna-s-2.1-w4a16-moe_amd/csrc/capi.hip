@@ -375,6 +375,9 @@ GemvLaunch gemv_args(const FusedArgs& a, const Layout& L, const Work& w, int mod
     g.ids = a.ids;
     g.max_items = (int32_t)L.max_items;
     g.dropped_out = w.header + 1;
+    // the item -> expert list of the w13 launch for the w2 launch, in the
+    // sorted-ids region, which no self-routed call uses (EM >= n_tok)
+    g.route_items = w.sorted;
   }
   if (mode == 0) {
     g.act = static_cast<const uint16_t*>(a.hidden);

@@ -177,6 +177,10 @@ struct GemvLaunch {
                            // launcher, else 1, 2 or 4 (1 for run-time loops)
   int32_t lpr;             // lanes per weight row: 0 = chosen by the launcher,
                            // else 8 or 32 (32 for passes of at most 2 tokens)
+  // Self-routing: the expert of every work item (-1: none), [max_items];
+  // written by the w13 launch, read by the w2 launch.  Null: each launch
+  // routes on its own.
+  int32_t* route_items;
 };
 hipError_t launch_w13_gemv(const GemvLaunch& a, hipStream_t stream);
 hipError_t launch_w2_gemv(const GemvLaunch& a, hipStream_t stream);

@@ -157,15 +157,17 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
 // experts) its end, where they hold a slot in the launch's tail rather than
 // among the streaming workgroups: M=16 123.0 -> 121.8 us per call, M=12
 // 102.8 -> 102.2, skewed M=8, 12, 16 57.2 -> 56.1, 72.4 -> 70.8, 93.2 ->
-// 91.8.  The same search on the shorter w2 workgroups cost more than it
-// saved (uniform M=8, 12, 16: +1.0, +1.5, +0.2 us), and below 65 pairs on
-// both (M=2 25.9 -> 26.6).  tab: this wave's
-// E ints of LDS, where the first slot of every expert is a minimum over the
-// slots (a wave's LDS instructions run in order, so no wait separates the
-// steps).
+// 91.8.  Below 65 pairs the search cost more than the few empty items
+// (M=2 25.9 -> 26.6).  tab: this wave's E ints of LDS, where the first slot
+// of every expert is a minimum over the slots (a wave's LDS instructions run
+// in order, so no wait separates the steps).
+// FROM_ITEMS (the w2 launch, after a w13 launch that wrote a.route_items):
+// item `item` is w13's item `item`, whose expert (-1: no work) the w13
+// launch left in a.route_items; the same search on w2's shorter workgroups
+// cost more than it saved (uniform M=8, 12, 16: +1.0, +1.5, +0.2 us).
 // NQ: ids per lane actually read (1 when n_tok <= 64, else 4); the lanes'
 // further ids count as absent.
-template <int NQ, bool COMPACT>
+template <int NQ, bool COMPACT, bool FROM_ITEMS>
 __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e_out,
                                            int& t_out, int (&fl)[4], int& dropped, int* tab) {
   const int lane = __lane_id();
@@ -189,7 +191,10 @@ __device__ __forceinline__ void route_wave(const GemvLaunch& a, int item, int& e
   e_out = -1;
   t_out = 0;
   int e;
-  if (!COMPACT || NQ == 1 || n_tok <= a.topk) {
+  if (FROM_ITEMS) {
+    e = __builtin_amdgcn_readfirstlane(a.route_items[item]);
+    if (e < 0 || e >= E) return;
+  } else if (!COMPACT || NQ == 1 || n_tok <= a.topk) {
     e = __builtin_amdgcn_readfirstlane(a.ids[item]);
     if (e < 0 || e >= E) return;
     bool earlier = false;
@@ -316,11 +321,19 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
     int dropped;
     // this wave's routing table, past the staged rows (gemv_route_lds_bytes)
     int* tab = reinterpret_cast<int*>(xc + TC * xc_pitch) + wid * a.num_experts;
-    if (a.n_tok <= 64)
-      route_wave<1, MODE == 0>(a, item, e, T, fl, dropped, tab);
-    else
-      route_wave<4, MODE == 0>(a, item, e, T, fl, dropped, tab);
+    if (MODE == 1 && a.route_items) {
+      if (a.n_tok <= 64)
+        route_wave<1, false, true>(a, item, e, T, fl, dropped, tab);
+      else
+        route_wave<4, false, true>(a, item, e, T, fl, dropped, tab);
+    } else if (a.n_tok <= 64) {
+      route_wave<1, MODE == 0, false>(a, item, e, T, fl, dropped, tab);
+    } else {
+      route_wave<4, MODE == 0, false>(a, item, e, T, fl, dropped, tab);
+    }
     if (MODE == 0 && bid == 0 && tid == 0) a.dropped_out[0] = dropped;
+    // w13 leaves every item's expert (-1: no work) for the w2 launch
+    if (MODE == 0 && a.route_items && slab0 == 0 && tid == 0) a.route_items[item] = e;
     if (e < 0) return;  // workgroup-uniform: every wave routes the same item
   } else {
     int blk = item;
