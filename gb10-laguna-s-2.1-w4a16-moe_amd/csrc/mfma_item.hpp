@@ -220,8 +220,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //      16-byte bank groups of a 128-byte (256-byte) bank row.
 //   W  WSLOTS slots x NW waves x 2 KB: a wave's packed weights of a pair of
 //      double steps (64 bytes of each of its 32 rows), as two DMAs of 16
-//      rows: DMA h, lane l holds row 16 h + l / 4, bytes 16 (l % 4) of the
-//      pair's 64, at h * 1024 + l * 16.  The weights run 2 WSLOTS - 1 double
+//      rows: DMA h, lane l holds row r = 16 h + l / 4, bytes 16 c of the
+//      pair's 64, c = (l % 4) ^ ((r % 16) / 4), at h * 1024 + l * 16 (the
+//      swizzle spreads a read of 16 rows over all banks).  The weights run 2 WSLOTS - 1 double
 //      steps ahead, deeper than the activations: they come from HBM, the
 //      activation rows mostly from L2.
 //   S  2 slots x NW waves x 512 B: a wave's scales of one loop iteration (8
@@ -421,14 +422,24 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   const int64_t e_rows = (int64_t)e * rows_total;
   const char* const wexp = reinterpret_cast<const char*>(a.w) + e_rows * (kdim / 2);
   const char* const sexp = reinterpret_cast<const char*>(a.s) + e_rows * gpr * 2;
-  // Weight DMA h of a pair: this lane fetches bytes 16 (lane % 4) of the
-  // pair's 64 of local row 16 h + lane / 4.
+  // Weight DMA h of a pair: lane l lands at LDS position l (16 bytes each) of
+  // the DMA's kilobyte: row r = 16 h + l / 4, slot l % 4 of the row's 64
+  // bytes, which holds the row's 16-byte group (l % 4) ^ sw(r % 16),
+  // sw(r) = (r / 4) % 4.  The reads below take one group of 16 rows at once,
+  // 64 bytes apart: without the swizzle four of those rows share every bank
+  // (LDS banks repeat every 256 bytes).
+  auto wswz = [](int r) { return (r >> 2) & 3; };
   uint32_t w_off[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
-    w_off[h] = (uint32_t)wrow(16 * h + (lane >> 2)) * (uint32_t)(kdim / 2) + 16u * (lane & 3);
-  // Lane (j, q) reads 16-byte group 2 (t % 2) + q of row j's pair block.
-  const uint32_t w_rd = (uint32_t)((j >> 4) * 1024 + (j & 15) * 64 + q * 16);
+    w_off[h] = (uint32_t)wrow(16 * h + (lane >> 2)) * (uint32_t)(kdim / 2) +
+               16u * (uint32_t)((lane & 3) ^ wswz(lane >> 2));
+  // Lane (j, q) reads 16-byte group 2 (t % 2) + q of row j's pair block, at
+  // slot group ^ sw(j % 16): w_rd[t % 2].
+  uint32_t w_rd[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+    w_rd[b] = (uint32_t)((j >> 4) * 1024 + (j & 15) * 64 + 16 * ((2 * b + q) ^ wswz(j & 15)));
   const uint32_t s_off = (uint32_t)grow * (uint32_t)gpr * 2u;
   unsigned char* const w_lds = lds + G::kOffW + wid * 2048;  // + slot * kWslot
   unsigned char* const s_lds = lds + G::kOffS + wid * 512;   // + slot * kSslot
@@ -506,7 +517,7 @@ __device__ __forceinline__ void run_tile(const MfmaLaunch& a, int e, int nt0, in
   // The step's weight words (pair slot wsl) and scale word (this wave's own
   // DMAs).
   auto read_w_operands = [&](int tp, int wsl, int sslot) {
-    wq_next = *reinterpret_cast<const u32x4_t*>(w_lds + wsl * kWslot + w_rd + (tp & 1) * 32);
+    wq_next = *reinterpret_cast<const u32x4_t*>(w_lds + wsl * kWslot + w_rd[tp & 1]);
     sw_next = scale_word(sslot, tp);
   };
   // Group constants and k-step 0 weights of the step whose words were read.
