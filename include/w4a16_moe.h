@@ -73,9 +73,10 @@ extern "C" {
 #define W4A16_WS_NFIELDS      8
 /* Calls with M <= W4A16_GEMV_ONLY_MAX_M skip the align kernel: the GEMV
  * kernels route themselves from topk_ids.  Those calls write only the
- * header's dropped count [1], INTER and PARTIAL (not PARTIAL when M <= 4: w2
- * and the top-k sum then run as one kernel); the other fields keep whatever
- * they held. */
+ * header's dropped count [1], INTER, PARTIAL (not PARTIAL when M <= 4: w2
+ * and the top-k sum then run as one kernel) and, in the first M*topk entries
+ * of SORTED_IDS, the w13 launch's expert of each work item (-1: none), which
+ * the w2 launch reads; the other fields keep whatever they held. */
 
 /* Token-block size the fused call uses for its internal expert sort. */
 #define W4A16_FUSED_BLOCK_M 16
