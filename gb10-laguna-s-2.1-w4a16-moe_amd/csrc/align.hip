@@ -493,11 +493,21 @@ __global__ __launch_bounds__(kChunk) void align_place_kernel(const AlignLaunch a
     const int e = tid - part * E;
     if (part < parts) {
       int before = 0, all = 0;
-#pragma unroll 4
-      for (int c = part; c < n_chunks; c += parts) {
-        const int v = ctot[(int64_t)c * E + e];
-        before += c < g ? v : 0;
-        all += v;
+      // 16 chunks' counts in flight per round trip (a batch of 40 chunks,
+      // M=4096, is one round trip on four parts)
+      constexpr int kLoads = 16;
+      for (int c0 = part; c0 < n_chunks; c0 += kLoads * parts) {
+        int v[kLoads];
+#pragma unroll
+        for (int b = 0; b < kLoads; ++b) {
+          const int c = c0 + b * parts;
+          v[b] = c < n_chunks ? ctot[(int64_t)c * E + e] : 0;
+        }
+#pragma unroll
+        for (int b = 0; b < kLoads; ++b) {
+          before += c0 + b * parts < g ? v[b] : 0;
+          all += v[b];
+        }
       }
       atomicAdd(&tot[e], all);
       atomicAdd(&off[e], before);  // parked here until the offsets are known
