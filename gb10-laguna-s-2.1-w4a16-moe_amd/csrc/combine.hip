@@ -19,6 +19,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Slots whose partial loads are in flight together.
 constexpr int kSlotBatch = 16;
 constexpr int kCombineThreads = 128;
+// From this many bytes of partial rows the loads are non-temporal: M=4096
+// combine 51.3 -> 47.1 us, skewed M=64 (3.9 MB) 3.70 -> 3.54 us; M=16's
+// 1 MB, still in L2 from the w2 launch, read 3.12 -> 3.47 us with the hint.
+constexpr int64_t kCombineNtBytes = 2 << 20;
 
 // One thread owns VPT consecutive outputs of one token (8 for bf16 partials,
 // 4 for fp32: one 16-byte load per slot).  The ids of a batch of slots are
@@ -26,7 +30,7 @@ constexpr int kCombineThreads = 128;
 // unwritten row: it is read and left out), all in flight together, and the
 // values are added in slot order from +0.0 -- the order of the reference's
 // sum, so the result does not depend on the batching.
-template <bool VEC_STORE, bool BF16>
+template <bool VEC_STORE, bool BF16, bool NT>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineLaunch a) {
   constexpr int VPT = BF16 ? 8 : 4;
   const int per_row = a.K / VPT;
@@ -51,7 +55,9 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineL
       if (j < nb) {  // uniform
         const int e = a.ids[row0 + t0 + j];
         ok[j] = e >= 0 && e < a.num_experts;
-        v[j] = *reinterpret_cast<const u32x4_t*>(base + (size_t)(row0 + t0 + j) * row_bytes);
+        const u32x4_t* src =
+            reinterpret_cast<const u32x4_t*>(base + (size_t)(row0 + t0 + j) * row_bytes);
+        v[j] = NT ? __builtin_nontemporal_load(src) : *src;
       }
     }
 #pragma unroll
@@ -85,12 +91,12 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineL
   }
 }
 
-template <bool BF16>
+template <bool BF16, bool NT>
 void launch_combine_t(const CombineLaunch& a, dim3 grid, bool vec, hipStream_t stream) {
   if (vec)
-    hipLaunchKernelGGL((combine_kernel<true, BF16>), grid, dim3(kCombineThreads), 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<true, BF16, NT>), grid, dim3(kCombineThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((combine_kernel<false, BF16>), grid, dim3(kCombineThreads), 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<false, BF16, NT>), grid, dim3(kCombineThreads), 0, stream, a);
 }
 
 }  // namespace
@@ -104,10 +110,18 @@ hipError_t launch_combine(const CombineLaunch& a, hipStream_t stream) {
   const int64_t kchunks = (a.K / vpt + kCombineThreads - 1) / kCombineThreads;
   const dim3 grid((unsigned)(kchunks * a.M));
   const bool vec = (reinterpret_cast<uintptr_t>(a.out) % (2 * vpt) == 0) && (a.ld_out % vpt == 0);
-  if (a.partial_bf16)
-    launch_combine_t<true>(a, grid, vec, stream);
-  else
-    launch_combine_t<false>(a, grid, vec, stream);
+  const bool nt = (int64_t)a.M * a.topk * a.K * (a.partial_bf16 ? 2 : 4) >= kCombineNtBytes;
+  if (a.partial_bf16) {
+    if (nt)
+      launch_combine_t<true, true>(a, grid, vec, stream);
+    else
+      launch_combine_t<true, false>(a, grid, vec, stream);
+  } else {
+    if (nt)
+      launch_combine_t<false, true>(a, grid, vec, stream);
+    else
+      launch_combine_t<false, false>(a, grid, vec, stream);
+  }
   return hipGetLastError();
 }
 
