@@ -101,7 +101,8 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
         const int gi = min(it * 8 + sl, G - 1);
-        wq[j][it] = *reinterpret_cast<const u32x4_t*>(wrow + j * wstep + gi * 16);
+        wq[j][it] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(wrow + j * wstep + gi * 16));
         sq[j][it] = *reinterpret_cast<const uint16_t*>(srow + j * sstep + (gi >> gshift) * 2);
       }
   }
@@ -135,7 +136,8 @@ __global__ __launch_bounds__(1024) void w2_token_kernel(const GemvLaunch a, uint
     } else {
       for (int it = 0; it < n_it; ++it) {
         const int gi = min(it * 8 + sl, G - 1);
-        const u32x4_t w4 = *reinterpret_cast<const u32x4_t*>(wrow + j * wstep + gi * 16);
+        const u32x4_t w4 = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(wrow + j * wstep + gi * 16));
         const uint32_t sb =
             *reinterpret_cast<const uint16_t*>(srow + j * sstep + (gi >> gshift) * 2);
         step(w4, sb, it, acc);

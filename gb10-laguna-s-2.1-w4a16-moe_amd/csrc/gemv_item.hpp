@@ -429,9 +429,15 @@ __device__ __forceinline__ void gemv_item(const GemvLaunch a, int bid, u32x4_t* 
         dw = drow * (uint32_t)G * 16u;
         ds = drow * (uint32_t)gpr * 2u;
       }
+      // Non-temporal weight loads: every 128-byte line is read whole by one
+      // instruction (8 lanes of a row) and never again in the call, so it
+      // need not displace cached lines (M=16 120.5 -> 109.6 us per call,
+      // M=1 15.86 -> 15.13).  The scales' lines are read in pieces over 8
+      // steps and keep the default policy.
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        wq[j] = *reinterpret_cast<const u32x4_t*>(wexp + (woff[j] + dw + gi * 16u));
+        wq[j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(wexp + (woff[j] + dw + gi * 16u)));
         sq[j] = *reinterpret_cast<const uint16_t*>(sexp + (soff[j] + ds + (gi >> gshift) * 2u));
       }
     };
