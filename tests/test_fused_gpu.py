@@ -461,13 +461,13 @@ def test_full_size_configs(pkg, orc, synth, dev, full_layer, cfg_index, dispatch
            bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K, tuning))
 
 
-@pytest.mark.parametrize("M,skewed", [(2, False), (3, True), (8, True), (24, False), (24, True),
-                                      (28, True), (48, True)])
+@pytest.mark.parametrize("M,skewed", [(2, False), (3, True), (8, True), (20, False), (20, True),
+                                      (24, False), (24, True), (28, True), (48, True)])
 def test_full_size_table_entries(pkg, orc, synth, dev, full_layer, M, skewed):
     """Every output row at full size under the committed table's entry for M
     (nearest key): the decode and small-batch entries, which the benchmark
     configurations do not reach (M=2-3 GEMV-only with two 32-lane rows per
-    pass, M=21-28 the split with a 2-pair threshold)."""
+    pass, M=19-28 the split with a 2-pair threshold)."""
     shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
     tuning = _dispatch(pkg, "table", M, shape, dev)
     print(f"full-size M={M} skewed={skewed} (table: {tuning})", flush=True)
