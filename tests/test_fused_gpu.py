@@ -487,6 +487,28 @@ def test_full_size_table_entries(pkg, orc, synth, dev, full_layer, M, skewed):
            mismatch_max=flips)
 
 
+@pytest.mark.parametrize("M,skewed", [(37, True), (333, False), (777, True), (2222, False),
+                                      (5000, True)])
+def test_full_size_odd_batches(pkg, orc, synth, dev, full_layer, M, skewed):
+    """Every output row at full size for batch sizes between the benchmark's,
+    under the built-in dispatch: 64-slot tiles in mixed launches (M=37, 333),
+    128-slot tiles (M=777), 192-slot tiles with the many-workgroup sort
+    (M=2222) and experts cut into two tiles (M=5000, skewed), with 1 % of
+    the ids set outside [0, E) (skipped by the sort and the sum)."""
+    shape, (w13, w2, s13, s2), (c13, c2, cs13, cs2) = full_layer
+    print(f"full-size odd batch M={M} skewed={skewed}", flush=True)
+    x = synth.make_hidden(M, shape.K, dev, seed=M)
+    tw, ti = synth.make_routing(M, shape.E, shape.topk, dev, seed=M, skewed=skewed)
+    g = torch.Generator().manual_seed(M)
+    drop = (torch.rand(ti.shape, generator=g) < 0.01).to(dev)
+    ti = torch.where(drop, torch.full_like(ti, -1), ti).contiguous()
+    out = pkg.fused_experts_w4a16(x, w13, w2, s13, s2, tw, ti, 32)
+    torch.cuda.synchronize()
+    _check(orc, out, x.cpu(), c13, c2, cs13, cs2, tw.cpu(), ti.cpu(), 32,
+           f"odd batch M={M} skewed={skewed}",
+           bf16_experts=mfma_experts(pkg, ti, shape.E, shape.N, shape.K))
+
+
 def test_reference_bench_magnitudes_max_abs(pkg, orc, synth, dev):
     """max-abs <= 2e-2 at the reference bench's magnitudes (x/10, w ~ randn/10)."""
     shape = synth.LayerShape()
